@@ -1,0 +1,158 @@
+"""Python face of the oracle (TEST INFRASTRUCTURE ONLY).
+
+Wraps the C restatement in ``oracle/w8a8_oracle.c`` (built into
+``oracle/liboracle.so`` by ``oracle/Makefile``) with numpy arrays.  Only
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` import this module, and only to check or time the reference's
+algorithm; the product library never does.
+
+16-bit floating tensors travel as ``np.uint16`` bit arrays next to a dtype
+name: ``"f32"`` (np.float32 values), ``"f16"`` or ``"bf16"`` (np.uint16 bits).
+"""
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+DTYPE_CODE = {"f32": 0, "f16": 1, "bf16": 2}
+
+_lib = None
+
+
+def build():
+    """Compile the C restatement with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "liboracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB_PATH))
+        f = _lib
+        p, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        f.w8o_quant_rowwise.argtypes = [p, i32, i64, i64, i32, i32, p, p]
+        f.w8o_gemm_i32.argtypes = [p, p, i64, i64, i64, p]
+        f.w8o_epilogue_kitchen.argtypes = [p, p, p, i64, p, p, i32, i64, i64, i32, i32]
+        f.w8o_epilogue_eager.argtypes = [p, p, p, i64, p, p, i32, i64, i64]
+        f.w8o_gelu_tanh_tensor.argtypes = [p, p, i32, i64]
+        f.w8o_f32_to_bf16_n.argtypes = [p, p, i64]
+        f.w8o_f32_to_f16_n.argtypes = [p, p, i64]
+        f.w8o_gelu_tanh.argtypes = [ctypes.c_float]
+        f.w8o_gelu_tanh.restype = ctypes.c_float
+        f.w8o_round_to.argtypes = [ctypes.c_float, i32]
+        f.w8o_round_to.restype = ctypes.c_float
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def _storage(dtype):
+    return np.float32 if dtype == "f32" else np.uint16
+
+
+def to_dtype(values_f32, dtype):
+    """Round float32 values to ``dtype`` storage (bits for 16-bit types), RNE."""
+    v = np.ascontiguousarray(values_f32, dtype=np.float32)
+    if dtype == "f32":
+        return v.copy()
+    out = np.empty(v.shape, np.uint16)
+    fn = lib().w8o_f32_to_bf16_n if dtype == "bf16" else lib().w8o_f32_to_f16_n
+    fn(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+def to_f32(storage, dtype):
+    """Widen a tensor held in ``dtype`` storage to float32 values (exact)."""
+    s = np.ascontiguousarray(storage)
+    if dtype == "f32":
+        return s.astype(np.float32)
+    if dtype == "bf16":
+        return (s.astype(np.uint32) << 16).view(np.float32)
+    return s.view(np.float16).astype(np.float32)
+
+
+def quant_rowwise(x, dtype, scale_mode=0, act=0):
+    """Per-token absmax quantization of ``x`` [M, K] -> (q int8 [M, K], s fp32 [M]).
+
+    scale_mode 0: IEEE amax/127 (the reference's CPU/eager path);
+    scale_mode 1: amax * (1/127f) (the reference's CUDA kernel).
+    act 1 applies gelu_tanh to x (rounded to its dtype) before quantizing.
+    """
+    x = np.ascontiguousarray(x, dtype=_storage(dtype))
+    M, K = x.shape
+    q = np.empty((M, K), np.int8)
+    s = np.empty((M,), np.float32)
+    lib().w8o_quant_rowwise(_ptr(x), DTYPE_CODE[dtype], M, K, scale_mode, act, _ptr(q), _ptr(s))
+    return q, s
+
+
+def gemm_i32(a, b):
+    """Exact int32 C = A @ B.T for int8 A [M, K], B [N, K]."""
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.int8)
+    M, K = a.shape
+    N, K2 = b.shape
+    assert K == K2
+    c = np.empty((M, N), np.int32)
+    lib().w8o_gemm_i32(_ptr(a), _ptr(b), M, N, K, _ptr(c))
+    return c
+
+
+def epilogue_kitchen(acc, xs, ws, bias, out_dtype, contract=1, act=0):
+    """GPU-route dequant: O((float(acc)*xs)*ws + bias) with one rounding.
+
+    ``bias`` is in ``out_dtype`` storage or None; ``act`` 1 appends gelu_tanh.
+    """
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    M, N = acc.shape
+    xs = np.ascontiguousarray(xs, dtype=np.float32).reshape(-1)
+    ws = np.ascontiguousarray(ws, dtype=np.float32).reshape(-1)
+    assert xs.size == M and ws.size in (1, N)
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=_storage(out_dtype)).reshape(-1)
+        assert bias.size == N
+    out = np.empty((M, N), _storage(out_dtype))
+    lib().w8o_epilogue_kitchen(_ptr(acc), _ptr(xs), _ptr(ws), ws.size, _ptr(bias), _ptr(out),
+                               DTYPE_CODE[out_dtype], M, N, contract, act)
+    return out
+
+
+def epilogue_eager(acc, xs, ws, bias_f32, out_dtype):
+    """CPU-eager dequant: O(float(acc)*(xs*ws)) then + O(bias) in the output dtype."""
+    acc = np.ascontiguousarray(acc, dtype=np.int32)
+    M, N = acc.shape
+    xs = np.ascontiguousarray(xs, dtype=np.float32).reshape(-1)
+    ws = np.ascontiguousarray(ws, dtype=np.float32).reshape(-1)
+    if bias_f32 is not None:
+        bias_f32 = np.ascontiguousarray(bias_f32, dtype=np.float32).reshape(-1)
+    out = np.empty((M, N), _storage(out_dtype))
+    lib().w8o_epilogue_eager(_ptr(acc), _ptr(xs), _ptr(ws), ws.size, _ptr(bias_f32), _ptr(out),
+                             DTYPE_CODE[out_dtype], M, N)
+    return out
+
+
+def gelu_tanh(x, dtype):
+    """gelu_tanh of a tensor in ``dtype`` storage, rounded back to ``dtype``."""
+    x = np.ascontiguousarray(x, dtype=_storage(dtype))
+    y = np.empty_like(x)
+    lib().w8o_gelu_tanh_tensor(_ptr(x), _ptr(y), DTYPE_CODE[dtype], x.size)
+    return y
+
+
+def linear_kitchen(x, x_dtype, w, ws, bias, out_dtype, scale_mode=0, input_act=0,
+                   epilogue_act=0, contract=1):
+    """Composed GPU-route linear: quantize -> int32 GEMM -> single-rounding epilogue.
+
+    Returns (out, q, xs, acc) so callers can check every intermediate.
+    """
+    q, xs = quant_rowwise(x, x_dtype, scale_mode=scale_mode, act=input_act)
+    acc = gemm_i32(q, w)
+    out = epilogue_kitchen(acc, xs, ws, bias, out_dtype, contract=contract, act=epilogue_act)
+    return out, q, xs, acc

@@ -1,0 +1,253 @@
+/*
+ * w8a8_oracle.c -- CPU restatement of the reference's W8A8 linear family.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP kernels are
+ * compared against; nothing in the product library links, loads or calls it.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it.
+ *
+ * Plain C99, no dependencies, compiled with -O2 -ffp-contract=off so that every
+ * float operation below is exactly one IEEE-754 binary32 operation in the
+ * written order (the restatement must not be re-associated or contracted
+ * unless a function says it contracts on purpose).
+ *
+ * Dtype codes follow the reference's output-code convention
+ * (inference/src/cuda_linear.rs:488-497): 0 = fp32, 1 = fp16, 2 = bf16.
+ *
+ * Pinning (how each function is checked, see tests/test_oracle.py):
+ *   bf16/fp16 rounding   exhaustive against numpy's float16 and a brute-force
+ *                        nearest-even search; torch CPU casts.
+ *   w8o_quant_rowwise    reference golden vectors (int8 + scale bytes) from
+ *                        reference_primitives.py:357-365 and :388-391, and the
+ *                        1386 + 504 + 612 + 1728 end-to-end CUDA payloads.
+ *   w8o_gemm_i32         brute force in int64 (python ints) and the reference's
+ *                        int8_mm golden vectors (reference_int8_linear.py:18-30).
+ *   w8o_epilogue_kitchen reference CUDA payloads (GEMM/GEMV/M1 routes, all dtypes).
+ *   w8o_epilogue_eager   reference eager_int8_linear CPU payloads.
+ *   w8o_gelu_tanh        reference gelu_tanh activation payloads (1 bf16 ulp).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define W8O_F32 0
+#define W8O_F16 1
+#define W8O_BF16 2
+
+/* ------------------------------------------------------------------------ */
+/* Floating-point storage conversions (round to nearest even).             */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+uint16_t w8o_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u); /* quiet NaN */
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float w8o_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t w8o_f32_to_f16(float f) {
+    uint32_t u = f2u(f);
+    uint32_t sign = (u >> 16) & 0x8000u;
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to inf */
+    if (a < 0x38800000u) {                                    /* below 2^-14: subnormal half */
+        /* value = a_float; half subnormal unit is 2^-24. */
+        float v = u2f(a);
+        /* exact scaling by 2^24 then round-half-even to integer */
+        float s = v * 16777216.0f;                               /* exact (power of two) */
+        float r = rintf(s);                                      /* default mode: half-even */
+        return (uint16_t)(sign | (uint32_t)r);
+    }
+    uint32_t mant = a & 0x7fffffu;
+    uint32_t exp = (a >> 23) - 127 + 15;
+    uint32_t h = (exp << 10) | (mant >> 13);
+    uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1; /* carries into exponent correctly */
+    return (uint16_t)(sign | h);
+}
+
+float w8o_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t mant = h & 0x3ffu;
+    if (exp == 0) {
+        float v = (float)mant * (1.0f / 16777216.0f); /* exact */
+        return sign ? -v : v;
+    }
+    if (exp == 31) return u2f(sign | 0x7f800000u | (mant << 13));
+    return u2f(sign | ((exp - 15 + 127) << 23) | (mant << 13));
+}
+
+/* Load element i of a buffer of the given dtype as float (exact widening). */
+static inline float load_as_f32(const void* p, int dtype, int64_t i) {
+    switch (dtype) {
+        case W8O_F16: return w8o_f16_to_f32(((const uint16_t*)p)[i]);
+        case W8O_BF16: return w8o_bf16_to_f32(((const uint16_t*)p)[i]);
+        default: return ((const float*)p)[i];
+    }
+}
+
+/* Round a float to the given dtype and widen back (the value a tensor of that
+ * dtype would hold). */
+static inline float round_to(float v, int dtype) {
+    switch (dtype) {
+        case W8O_F16: return w8o_f16_to_f32(w8o_f32_to_f16(v));
+        case W8O_BF16: return w8o_bf16_to_f32(w8o_f32_to_bf16(v));
+        default: return v;
+    }
+}
+
+static inline void store_from_f32(void* p, int dtype, int64_t i, float v) {
+    switch (dtype) {
+        case W8O_F16: ((uint16_t*)p)[i] = w8o_f32_to_f16(v); break;
+        case W8O_BF16: ((uint16_t*)p)[i] = w8o_f32_to_bf16(v); break;
+        default: ((float*)p)[i] = v; break;
+    }
+}
+
+float w8o_round_to(float v, int dtype) { return round_to(v, dtype); }
+
+/* ------------------------------------------------------------------------ */
+/* GELU, tanh approximation, as ATen's CPU kernel orders it:
+ *   0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3)))
+ * Applied by the reference as input_act="gelu_tanh"
+ * (inference/src/int8_linear.rs:37-41 -> x.gelu("tanh")).  Computed in fp32 for
+ * 16-bit dtypes (ATen's opmath), result rounded to the tensor dtype. */
+float w8o_gelu_tanh(float x) {
+    const float kBeta = (float)(1.41421356237309504880 * 1.12837916709551257390 * 0.5);
+    const float kKappa = 0.044715f;
+    float x_cube = x * x * x;
+    float inner = kBeta * (x + kKappa * x_cube);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+/* ------------------------------------------------------------------------ */
+/* Per-token dynamic absmax INT8 quantization.
+ *
+ * Follows inference/src/eager.rs:159-171 (quantize_int8_rowwise_with_seed, no
+ * seed) with int8_scale_for_math (:94-109) and round_int8 (:110-121):
+ *   s  = clamp_min(float(amax_k |x_k|) / 127, 1e-30)         IEEE division
+ *   sT = dtype(s); if sT == 0: sT = tiny(dtype)
+ *   q  = int8(clamp(round_half_even(dtype(float(x) / float(sT))), -128, 127))
+ * scale_mode 1 replaces the scale by the Kitchen CUDA form
+ * fmaxf(fminf(amax, finite_max) * (1/127f), 1e-30)
+ * (native/comfy-port/kitchen/int8_linear.cu:36-39,205-208); the quotient
+ * (int8_linear.cu:47-51,214) is the same IEEE form in both modes.
+ * act 1 first applies gelu_tanh to x and rounds it to the dtype
+ * (inference/src/int8_linear.rs:37-41 then :198-199).
+ * x is [M, K] row-major; q is [M, K]; s is [M].  Finite inputs only. */
+void w8o_quant_rowwise(const void* x, int dtype, int64_t M, int64_t K, int scale_mode,
+                       int act, int8_t* q, float* s) {
+    const float finite_max = dtype == W8O_F16 ? 65504.0f
+                           : dtype == W8O_BF16 ? 3.38953139e38f : 3.40282347e38f;
+    const float tiny = dtype == W8O_F16 ? 6.103515625e-5f : 1.17549435e-38f;
+    for (int64_t m = 0; m < M; ++m) {
+        float amax = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            float v = load_as_f32(x, dtype, m * K + k);
+            if (act == 1) v = round_to(w8o_gelu_tanh(v), dtype);
+            float a = fabsf(v);
+            if (a > amax) amax = a;
+        }
+        float scale;
+        if (scale_mode == 1) {
+            float a = amax < finite_max ? amax : finite_max;
+            scale = a * (1.0f / 127.0f);
+        } else {
+            scale = amax / 127.0f;
+        }
+        if (!(scale >= 1e-30f)) scale = 1e-30f;
+        s[m] = scale;
+        float sT = round_to(scale, dtype);
+        if (sT == 0.0f) sT = tiny;
+        for (int64_t k = 0; k < K; ++k) {
+            float v = load_as_f32(x, dtype, m * K + k);
+            if (act == 1) v = round_to(w8o_gelu_tanh(v), dtype);
+            float quot = round_to(v / sT, dtype);
+            float r = rintf(quot); /* half-even in the default rounding mode */
+            if (r < -128.0f) r = -128.0f;
+            if (r > 127.0f) r = 127.0f;
+            q[m * K + k] = (int8_t)r;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* C[m, n] = sum_k A[m, k] * B[n, k] in int32 (exact: |C| <= K * 128 * 127 <
+ * 2^31 for K <= 132104).  A is [M, K], B is [N, K] row-major (the reference's
+ * weight layout, cutlass_gemm_int8.cu:71-72 "B[N,K] row == [K,N] col"). */
+void w8o_gemm_i32(const int8_t* A, const int8_t* B, int64_t M, int64_t N, int64_t K,
+                  int32_t* C) {
+    for (int64_t m = 0; m < M; ++m) {
+        const int8_t* a = A + m * K;
+        for (int64_t n = 0; n < N; ++n) {
+            const int8_t* b = B + n * K;
+            int32_t acc = 0;
+            for (int64_t k = 0; k < K; ++k) acc += (int32_t)a[k] * (int32_t)b[k];
+            C[m * N + n] = acc;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* The GPU routes' dequant epilogue, single rounding:
+ *   out = O( (float(acc) * xs[m]) * ws[n] + float(bias[n]) )
+ * CUTLASS EVT Mul0 -> Mul1 -> Add2 (cutlass_gemm_int8.cu:84-95), cuBLAS route
+ * dequantize_int8_linear_kernel (int8_linear.cu:517-541) and the GEMV kernels
+ * (int8_linear.cu:628-708).  bias is stored in the output dtype (the crate
+ * converts it, cuda_linear.rs:694-697) and may be NULL.  ws has ws_size 1
+ * (broadcast) or N entries.  contract = 1 evaluates the last multiply-add as
+ * one fused multiply-add, fmaf(float(acc) * xs, ws, bias), which is how nvcc's
+ * default --fmad=true compiles the reference's expression; contract = 0 rounds
+ * the product first.  act 1 appends gelu_tanh on the output-dtype value,
+ * out = O(gelu(float(O(lin)))), i.e. the next linear's input_act applied in
+ * the output dtype (int8_linear.rs:37-41).  xs has M entries. */
+void w8o_epilogue_kitchen(const int32_t* acc, const float* xs, const float* ws, int64_t ws_size,
+                          const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
+                          int contract, int act) {
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            float w = ws[ws_size == 1 ? 0 : n];
+            float b = bias ? load_as_f32(bias, out_dtype, n) : 0.0f;
+            float t = (float)acc[m * N + n] * xs[m];
+            float v = contract ? fmaf(t, w, b) : (t * w + b);
+            if (act == 1) v = w8o_gelu_tanh(round_to(v, out_dtype));
+            store_from_f32(out, out_dtype, m * N + n, v);
+        }
+    }
+}
+
+/* The CPU eager route's epilogue (inference/src/int8_linear.rs:240-269):
+ *   chunk = O( float(acc) * (xs[m] * ws[n]) )      scales multiplied first
+ *   out   = O( float(chunk) + float(O(bias[n])) )   bias added in the output dtype
+ * bias is given as fp32 values (the reference converts whatever dtype it has
+ * to the output dtype first, :263-269) and may be NULL. */
+void w8o_epilogue_eager(const int32_t* acc, const float* xs, const float* ws, int64_t ws_size,
+                        const float* bias, void* out, int out_dtype, int64_t M, int64_t N) {
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            float scale = xs[m] * ws[ws_size == 1 ? 0 : n];
+            float v = round_to((float)acc[m * N + n] * scale, out_dtype);
+            if (bias) v = round_to(v + round_to(bias[n], out_dtype), out_dtype);
+            store_from_f32(out, out_dtype, m * N + n, v);
+        }
+    }
+}
+
+/* Element-wise gelu_tanh on a tensor of the given dtype, result rounded to it. */
+void w8o_gelu_tanh_tensor(const void* x, void* y, int dtype, int64_t count) {
+    for (int64_t i = 0; i < count; ++i)
+        store_from_f32(y, dtype, i, w8o_gelu_tanh(load_as_f32(x, dtype, i)));
+}
+
+/* Bulk dtype conversions for the Python side. */
+void w8o_f32_to_bf16_n(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = w8o_f32_to_bf16(x[i]);
+}
+void w8o_f32_to_f16_n(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = w8o_f32_to_f16(x[i]);
+}

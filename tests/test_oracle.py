@@ -1,0 +1,248 @@
+"""Pin the oracle (CPU restatement) before trusting it.
+
+Every oracle function is checked against (a) the reference's own golden vectors
+and (b) independent facts: numpy/torch CPU rounding, brute-force integer
+arithmetic, the LibTorch-CPU op sequence the reference's CPU route issues.
+Several checks are run against a deliberately wrong variant too, to show the
+check can tell the difference.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from oracle import torch_eager as TE
+from tests.golden import fixtures as FX
+from tests.golden import operands as OP
+
+TORCH_DTYPE = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _to_torch(storage, dtype):
+    t = torch.from_numpy(np.ascontiguousarray(storage))
+    return t if dtype == "f32" else t.view(torch.int16).view(TORCH_DTYPE[dtype])
+
+
+def _tie_patterns(low_bits):
+    """All float32 bit patterns whose low bits below the 16-bit mantissa cut
+    equal one of the given values (ties, just below/above ties, exact)."""
+    hi = np.arange(1 << 19, dtype=np.uint32) << 13
+    pats = np.concatenate([hi | np.uint32(v) for v in low_bits])
+    return pats.view(np.float32)
+
+
+# ---------------------------------------------------------------- rounding
+
+
+def test_f16_rounding_matches_numpy_on_all_tie_classes():
+    vals = _tie_patterns([0, 1, 0x0FFF, 0x1000, 0x1001, 0x1FFF])
+    vals = vals[np.isfinite(vals)]
+    ours = O.to_dtype(vals, "f16")
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, ref)
+
+
+def test_bf16_rounding_matches_torch_on_all_tie_classes():
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    pats = np.concatenate([hi | np.uint32(v) for v in (0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF)])
+    vals = pats.view(np.float32)
+    vals = vals[np.isfinite(vals)]
+    ours = O.to_dtype(vals, "bf16")
+    ref = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, ref)
+
+
+# ---------------------------------------------------------------- quantizer
+
+
+def test_quant_matches_reference_rowwise_golden_vectors():
+    """reference_primitives.py:357-365: eager rowwise quant, CPU and CUDA devices,
+    zero first row.  CPU captures need the IEEE scale; CUDA-device eager captures
+    are reproduced by both forms on this data."""
+    n = 0
+    for c in FX.load()["int8_rowwise"]:
+        if c["seed"] is not None:
+            continue
+        xd = OP.dtype_name(c["dtype"])
+        x = O.to_dtype(OP.quantizer_x_primitives(), xd)
+        q, s = O.quant_rowwise(x, xd, scale_mode=0)
+        assert q.view(np.uint8).reshape(-1).tolist() == c["payload"], c
+        assert s.view(np.uint8).tolist() == c["scale"], c
+        n += 1
+    assert n == 6
+
+
+def test_quant_matches_reference_cuda_kernel_golden_vectors():
+    """reference_primitives.py:388-391: Kitchen's quantize_int8_rowwise kernel."""
+    cases = [c for c in FX.load()["native_int8_rowwise"] if c["seed"] is None]
+    assert len(cases) == 3
+    for c in cases:
+        xd = OP.dtype_name(c["dtype"])
+        q, s = O.quant_rowwise(O.to_dtype(OP.quantizer_x_native(), xd), xd, scale_mode=1)
+        assert q.view(np.uint8).reshape(-1).tolist() == c["payload"]
+        assert s.view(np.uint8).tolist() == c["scale"]
+
+
+def _student_t_outliers(m, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.distributions.StudentT(3.0).sample((m, k)) if False else None
+    # StudentT.sample has no generator argument; build t(3) from normals instead.
+    z = torch.randn(m, k, generator=g)
+    chi = torch.randn(m, k, 3, generator=g).pow(2).sum(-1)
+    x = z / torch.sqrt(chi / 3.0)
+    idx = torch.randperm(k, generator=g)[: max(1, k // 1000)]
+    x[:, idx] *= 50.0
+    return x
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("dist", ["normal", "student_t"])
+def test_quant_bit_exact_vs_libtorch_cpu_sequence(dtype, dist):
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(64, 3072, generator=g) if dist == "normal" else _student_t_outliers(64, 3072, 7)
+    x[3] = 0.0  # zero row exercises the 1e-30 clamp and the tiny substitution
+    xt = x.to(TORCH_DTYPE[dtype])
+    q_ref, s_ref = TE.quantize_rowwise(xt)
+    storage = xt.numpy() if dtype == "f32" else xt.view(torch.int16).numpy().view(np.uint16)
+    q, s = O.quant_rowwise(storage, dtype, scale_mode=0)
+    assert np.array_equal(q, q_ref.numpy())
+    assert np.array_equal(s.view(np.uint32), s_ref.reshape(-1).numpy().view(np.uint32))
+
+
+def test_quant_scale_forms_are_distinguished():
+    """The IEEE form and the reciprocal-multiply form differ on real data; the
+    LibTorch-CPU check above must fail for the wrong one."""
+    x = torch.randn(256, 512, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    _, s_ref = TE.quantize_rowwise(x)
+    _, s_wrong = O.quant_rowwise(x.view(torch.int16).numpy().view(np.uint16), "bf16", scale_mode=1)
+    assert not np.array_equal(s_wrong.view(np.uint32), s_ref.reshape(-1).numpy().view(np.uint32))
+
+
+def test_quant_with_gelu_input_act_vs_libtorch_cpu():
+    x = torch.randn(32, 1024, generator=torch.Generator().manual_seed(11)).to(torch.bfloat16)
+    xa = torch.nn.functional.gelu(x, approximate="tanh")
+    q_ref, s_ref = TE.quantize_rowwise(xa)
+    q, s = O.quant_rowwise(x.view(torch.int16).numpy().view(np.uint16), "bf16", act=1)
+    # gelu's tanh may differ by one fp32 ulp between libm and ATen's vector tanh;
+    # after bf16 rounding that almost never shows; require >= 99.99% exact codes.
+    assert (q != q_ref.numpy()).mean() < 1e-4
+    assert np.array_equal(s.view(np.uint32), s_ref.reshape(-1).numpy().view(np.uint32))
+
+
+# ---------------------------------------------------------------- GEMM
+
+
+def test_gemm_i32_brute_force_including_extremes():
+    rng = np.random.default_rng(0)
+    a = rng.integers(-128, 128, size=(7, 37), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-128, 128, size=(5, 37), dtype=np.int64).astype(np.int8)
+    a[0, :] = -128
+    b[0, :] = -128
+    c = O.gemm_i32(a, b)
+    ref = [[sum(int(a[i, k]) * int(b[j, k]) for k in range(37)) for j in range(5)] for i in range(7)]
+    assert c.tolist() == ref
+    assert c[0, 0] == 37 * 128 * 128
+
+
+def test_gemm_i32_matches_reference_int8_mm_golden_vectors():
+    n = 0
+    for c in FX.load()["int8_mm"]:
+        if "error" in c or c["m"] * c["n"] == 0:
+            continue
+        a, b = OP.int8_mm_operands(c["m"], c["k"], c["n"])
+        got = O.gemm_i32(a, np.ascontiguousarray(b.T))
+        assert got.reshape(-1).view(np.uint8).tolist() == c["payload"]
+        n += 1
+    assert n == 18
+
+
+def test_gemm_i32_matches_torch_int_mm():
+    g = torch.Generator().manual_seed(5)
+    a = torch.randint(-128, 128, (48, 256), generator=g, dtype=torch.int8)
+    b = torch.randint(-128, 128, (40, 256), generator=g, dtype=torch.int8)
+    ref = torch._int_mm(a, b.t().contiguous())
+    assert np.array_equal(O.gemm_i32(a.numpy(), b.numpy()), ref.numpy())
+
+
+# ---------------------------------------------------------------- epilogues
+
+
+@pytest.mark.parametrize("section", sorted(FX.SECTIONS))
+def test_kitchen_route_linear_matches_reference_cuda_payloads(section):
+    """Quantize -> int32 GEMM -> single-rounding epilogue reproduces every
+    no-residual, non-ConvRot Kitchen CUDA payload (GEMM, GEMV, M=1 and
+    input-activation routes; fp32/fp16/bf16 inputs and outputs)."""
+    n = 0
+    for c, ops in FX.linear_cases(section):
+        xd, od = OP.dtype_name(c["dtype"]), OP.dtype_name(c["output_dtype"])
+        x = O.to_dtype(ops["x"], xd)
+        x2 = x.reshape(-1, x.shape[-1])
+        ws = np.asarray(ops["scale"], np.float32).reshape(-1)
+        bias = None if ops["bias"] is None else O.to_dtype(np.asarray(ops["bias"], np.float32), od)
+        act = 1 if c.get("activation") == "gelu_tanh" else 0
+        out, _, _, _ = O.linear_kitchen(x2, xd, ops["weight"], ws, bias, od, input_act=act)
+        assert np.array_equal(out.reshape(-1), FX.payload(c, od)), c
+        n += 1
+    assert n > 100
+
+
+def test_eager_route_linear_matches_reference_eager_payloads():
+    """reference_int8_linear.py: eager int8_linear on CPU (IEEE scale) and on a
+    CUDA device (torch's CUDA division by a scalar multiplies by the reciprocal,
+    so those captures need the reciprocal scale form)."""
+    seen = {"cpu": 0, "cuda:0": 0}
+    for c in FX.load()["eager_int8_linear"]:
+        if "error" in c or c["mode"] not in ("plain", "gelu_tanh"):
+            continue
+        ops = OP.eager_linear_operands(c)
+        xd, od = OP.dtype_name(c["dtype"]), OP.dtype_name(c["output_dtype"])
+        x = O.to_dtype(ops["x"], xd)
+        mode = 0 if c["device"] == "cpu" else 1
+        q, xs = O.quant_rowwise(x.reshape(-1, x.shape[-1]), xd, scale_mode=mode,
+                                act=1 if c["mode"] == "gelu_tanh" else 0)
+        out = O.epilogue_eager(O.gemm_i32(q, ops["weight"]), xs, ops["scale"].astype(np.float32), None, od)
+        assert np.array_equal(out.reshape(-1), FX.payload(c, od)), c
+        seen[c["device"]] += 1
+    assert seen == {"cpu": 12, "cuda:0": 12}
+
+
+def test_eager_epilogue_bit_exact_vs_libtorch_cpu_with_bias():
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(33, 320, generator=g).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (70, 320), generator=g, dtype=torch.int8)
+    ws = torch.rand(70, generator=g) * 9e-3 + 1e-3
+    bias = (torch.randn(70, generator=g) * 0.02).to(torch.bfloat16)
+    out_ref, q_ref, xs_ref, acc_ref = TE.int8_linear(x, w, ws, bias, torch.bfloat16)
+    q, xs = O.quant_rowwise(x.view(torch.int16).numpy().view(np.uint16), "bf16")
+    acc = O.gemm_i32(q, w.numpy())
+    assert np.array_equal(acc, acc_ref.numpy())
+    out = O.epilogue_eager(acc, xs, ws.numpy(), bias.float().numpy(), "bf16")
+    assert np.array_equal(out, out_ref.view(torch.int16).numpy().view(np.uint16))
+    # The GPU-route single rounding differs from the eager double rounding
+    # somewhere, by at most one bf16 ulp at the magnitude of the larger of the
+    # result and the pre-bias value (the eager route rounds that one first).
+    single = O.epilogue_kitchen(acc, xs, ws.numpy(), bias.view(torch.int16).numpy().view(np.uint16), "bf16")
+    pre = O.epilogue_eager(acc, xs, ws.numpy(), None, "f32")
+    a, b = O.to_f32(single, "bf16"), O.to_f32(out, "bf16")
+    mag = np.maximum(np.abs(b), np.abs(pre))
+    assert (np.abs(a - b) <= mag * 2.0**-7).all()
+    assert (single != out).any()
+
+
+def test_gelu_tanh_within_one_bf16_ulp_of_aten_on_every_bf16_value():
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    vals = O.to_f32(bits, "bf16")
+    keep = np.isfinite(vals)
+    bits = bits[keep]
+    ours = O.gelu_tanh(bits, "bf16")
+    ref = torch.nn.functional.gelu(_to_torch(bits, "bf16"), approximate="tanh")
+    ref = ref.view(torch.int16).numpy().view(np.uint16)
+    a = O.to_f32(ours, "bf16").astype(np.float64)
+    b = O.to_f32(ref, "bf16").astype(np.float64)
+    # One bf16 ulp, plus an absolute 2^-22 for the negative tail where
+    # 1 + tanh(u) is below fp32 resolution and ATen's vector tanh saturates to
+    # -1 a little earlier than libm (x ~ -5.1 gives -0.0 vs -1.5e-7).
+    tol = np.abs(b) * 2.0**-7 + 2.0**-22
+    assert (np.abs(a - b) <= tol).all()
+    assert (ours == ref).mean() > 0.9999
