@@ -1,0 +1,339 @@
+"""Benchmark of the W8A8 linear family on one MI355X.
+
+Default workload ("step"): one pass of the Qwen-Image-style DiT block's linear
+set at 1600x896 with CFG, M = 2 x (5600 + 256) = 11712 tokens, hidden 3072:
+  quantize -> QKV GEMM (N=9216), quantize -> out-proj (N=3072),
+  quantize -> FFN-up GEMM (N=12288, GELU-tanh fused epilogue),
+  quantize -> FFN-down GEMM (K=12288, N=3072).
+Synthetic seeded inputs (bf16 N(0,1) activations, int8 U[-127,127] weights,
+fp32 per-channel scales U(1e-3,1e-2), bf16 bias N(0,0.02)), resident in HBM.
+value = GEMM TOPS of the whole step (2*M*N*K summed over the 4 linears,
+divided by the step time, quantization included in the time).
+
+Also measured and reported beside it: per-linear TOPS, the per-token
+quantizer's GB/s (M=11712, K=3072 and K=12288), the adaLN GEMV's GB/s
+(M=2, K=3072, N=18432), and fused vs unfused quant+GEMM on the outlier
+workload (M=11712, K=3072, N=12288, Student-t(3) activations).  The memory-
+bound kernels rotate through enough buffer sets to exceed the 256 MB Infinity
+Cache so they measure HBM, not cache.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--only KERNEL] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+PEAK_INT8_TOPS = 5000.0       # MI355X dense INT8 MFMA, TOPS
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E, GB/s
+M_TOK = 2 * (5600 + 256)      # 11712
+HID, FFN, QKV = 3072, 12288, 9216
+LINEARS = [("qkv", HID, QKV, False), ("out", HID, HID, False), ("up", HID, FFN, True),
+           ("down", FFN, HID, False)]  # (name, K, N, gelu epilogue)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--only", default=None,
+                   help="run only one kernel in a loop (for rocprofv3 counters): "
+                        "up_gemm | quant | gemv | xq_gemm")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    return p.parse_args()
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def make_linear(k, n, seed, dev):
+    g = gen(seed)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    ws = torch.rand(n, generator=g) * 9e-3 + 1e-3
+    b = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    return w.to(dev), ws.to(dev), b.to(dev)
+
+
+def student_t(m, k, seed):
+    g = gen(seed)
+    z = torch.randn(m, k, generator=g)
+    chi = torch.randn(m, k, 3, generator=g).pow(2).sum(-1)
+    x = z / torch.sqrt(chi / 3.0)
+    idx = torch.randperm(k, generator=g)[: max(1, k // 1000)]
+    x[:, idx] *= 50.0
+    return x.to(torch.bfloat16)
+
+
+class Timer:
+    """HIP events on torch's current stream (the stream every W8A8 kernel is
+    launched on): per-launch durations of one kernel inside the timed region."""
+
+    def __init__(self):
+        self.pairs = []
+
+    def start(self):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+    def stop(self, s):
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append((s, e))
+
+    def mean_ms(self):
+        return statistics.fmean(s.elapsed_time(e) for s, e in self.pairs)
+
+
+def median_of_batches(fn, warmup=20, batches=7, calls=30):
+    """The reference's timing method: 20 warmups, 7 batches x 30 calls,
+    median of batch means (experiments/.../INT8-KITCHEN.md:35-39)."""
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    means = []
+    i = 0
+    for _ in range(batches):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(calls):
+            fn(i)
+            i += 1
+        e.record()
+        torch.cuda.synchronize()
+        means.append(s.elapsed_time(e) / calls)
+    return statistics.median(means)
+
+
+def cpu_baseline(seconds):
+    """The reference's LibTorch-CPU route (oracle/torch_eager.py, same ATen op
+    sequence as inference/src/int8_linear.rs:198-277) on a bounded sample of the
+    same workload: the 4 block linears at M=256 rows, repeated for ~`seconds`."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import torch_eager as TE
+    torch.set_num_threads(os.cpu_count() or 1)
+    m = 256
+    ops_per_pass = 0
+    layers = []
+    for i, (name, k, n, gelu) in enumerate(LINEARS):
+        w, ws, b = make_linear(k, n, 100 + i, "cpu")
+        x = torch.randn(m, k, generator=gen(200 + i)).to(torch.bfloat16)
+        layers.append((x, w, ws, b))
+        ops_per_pass += 2 * m * k * n
+    def one_pass():
+        for x, w, ws, b in layers:
+            TE.int8_linear(x, w, ws, b, torch.bfloat16)
+    one_pass()  # warmup
+    t0 = time.perf_counter()
+    passes = 0
+    while True:
+        one_pass()
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    tops = ops_per_pass * passes / el / 1e12
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(tops, 4), "unit": "TOPS", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"block linear set (QKV, out, up, down) at M=256 tokens, {passes} passes "
+                      f"in {el:.1f} s, LibTorch CPU int8_linear op sequence; host {model}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import imagine_amd as W
+    W._lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    print(f"[bench] device {torch.cuda.get_device_name(0)}", file=sys.stderr, flush=True)
+
+    # ---- block linear set operands
+    layers = []
+    for i, (name, k, n, gelu) in enumerate(LINEARS):
+        w, ws, b = make_linear(k, n, 10 + i, dev)
+        layers.append((name, k, n, gelu, w, ws, b))
+    x_qkv = torch.randn(M_TOK, HID, generator=gen(1)).to(torch.bfloat16).to(dev)
+    x_out = torch.randn(M_TOK, HID, generator=gen(2)).to(torch.bfloat16).to(dev)
+    x_ffn = torch.randn(M_TOK, HID, generator=gen(3)).to(torch.bfloat16).to(dev)
+    qbuf = {k: torch.empty((M_TOK, k), dtype=torch.int8, device=dev) for k in (HID, FFN)}
+    sbuf = torch.empty((M_TOK, 1), dtype=torch.float32, device=dev)
+    outs = {name: torch.empty((M_TOK, n), dtype=torch.bfloat16, device=dev) for name, _, n, *_ in layers}
+    lib = W._lib.load()
+    stream = lambda: torch.cuda.current_stream().cuda_stream
+
+    def quant(x, q):
+        W._lib.check(lib.w8a8_quantize_rowwise(x.data_ptr(), W._lib.BF16, q.data_ptr(), sbuf.data_ptr(),
+                                               x.shape[0], x.shape[1], 0, stream()))
+
+    def gemm(q, layer, out, gelu):
+        name, k, n, _, w, ws, b = layer
+        W._lib.check(lib.w8a8_gemm_dequant(q.data_ptr(), w.data_ptr(), sbuf.data_ptr(), ws.data_ptr(), n,
+                                           b.data_ptr(), out.data_ptr(), W._lib.BF16, M_TOK, n, k,
+                                           W._lib.ACT_GELU_TANH if gelu else 0, stream()))
+
+    up_timer = Timer()
+
+    def step(timed=False):
+        quant(x_qkv, qbuf[HID]); gemm(qbuf[HID], layers[0], outs["qkv"], False)
+        quant(x_out, qbuf[HID]); gemm(qbuf[HID], layers[1], outs["out"], False)
+        quant(x_ffn, qbuf[HID])
+        s = up_timer.start() if timed else None
+        gemm(qbuf[HID], layers[2], outs["up"], True)
+        if timed:
+            up_timer.stop(s)
+        quant(outs["up"], qbuf[FFN]); gemm(qbuf[FFN], layers[3], outs["down"], False)
+
+    if args.only:
+        run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs)
+        return
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(timed=True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    step_ops = sum(2 * M_TOK * k * n for _, k, n, *_ in LINEARS)
+    value = step_ops / (ms_per_step * 1e-3) / 1e12
+    up_ops = 2 * M_TOK * HID * FFN
+    up_ms = up_timer.mean_ms()
+    up_tops = up_ops / (up_ms * 1e-3) / 1e12
+    print(f"[bench] step {ms_per_step:.3f} ms -> {value:.1f} TOPS; up GEMM {up_ms*1e3:.1f} us "
+          f"-> {up_tops:.1f} TOPS", file=sys.stderr, flush=True)
+
+    extras = measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv)
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": "W8A8 GEMM TOPS (% INT8 MFMA peak) at Qwen-DiT 1600x896 shapes; quant GB/s",
+        "value": round(value, 2), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "qwen_dit_block_linear_set_1600x896_cfg", "M": M_TOK, "hidden": HID,
+                   "ffn": FFN, "linears": "qkv 3072->9216, out 3072->3072, up 3072->12288 +gelu_tanh, "
+                                         "down 12288->3072; per-token quant of each input included",
+                   "parallelism": "single_gpu", "pct_int8_peak": round(100 * value / PEAK_INT8_TOPS, 2)},
+        "roofline": {"kernel": "gemm_mfma (FFN-up 11712x3072x12288, bf16 out, GELU epilogue)",
+                     "bound": "mfma", "achieved": round(up_tops, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TOPS", "frac": round(up_tops / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "launch_us": round(up_ms * 1e3, 2), "algorithmic_ops": up_ops},
+        "cpu_baseline": cpu,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv):
+    ex = {}
+    stream = lambda: torch.cuda.current_stream().cuda_stream
+    # per-linear GEMM (no quant), reference timing method
+    for layer in layers:
+        name, k, n, gelu, *_ = layer
+        q = qbuf[k]
+        ms = median_of_batches(lambda i: gemm(q, layer, outs[name], gelu), warmup=5, batches=5, calls=10)
+        tops = 2 * M_TOK * k * n / (ms * 1e-3) / 1e12
+        ex[f"gemm_{name}"] = {"us": round(ms * 1e3, 1), "TOPS": round(tops, 1),
+                              "pct_peak": round(100 * tops / PEAK_INT8_TOPS, 1)}
+    # quantizer GB/s, rotating input sets past the Infinity Cache
+    for k in (HID, FFN):
+        per = 2 * M_TOK * k + M_TOK * k + 4 * M_TOK
+        nsets = max(2, int(1.2e9 // per) + 1)
+        xs = [torch.randn(M_TOK, k, device=dev, dtype=torch.bfloat16) for _ in range(nsets)]
+        qs = [torch.empty(M_TOK, k, dtype=torch.int8, device=dev) for _ in range(nsets)]
+        ss = torch.empty(M_TOK, dtype=torch.float32, device=dev)
+        def run(i):
+            j = i % nsets
+            W._lib.check(lib.w8a8_quantize_rowwise(xs[j].data_ptr(), W._lib.BF16, qs[j].data_ptr(),
+                                                   ss.data_ptr(), M_TOK, k, 0, stream()))
+        ms = median_of_batches(run)
+        ex[f"quant_K{k}"] = {"us": round(ms * 1e3, 2), "GB/s": round(per / (ms * 1e-3) / 1e9, 1),
+                             "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+                             "bytes": per, "buffer_sets": nsets}
+        del xs, qs
+    # adaLN GEMV, M=2 K=3072 N=18432, rotating weights
+    m, k, n = 2, 3072, 18432
+    per = n * k + 4 * n + 2 * m * k + 2 * m * n + 2 * n
+    nsets = max(2, int(1.2e9 // per) + 1)
+    ws_ = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev) for _ in range(nsets)]
+    wsc = torch.rand(n, device=dev) * 9e-3 + 1e-3
+    bias = (torch.randn(n, device=dev) * 0.02).to(torch.bfloat16)
+    xsil = torch.nn.functional.silu(torch.randn(m, k, device=dev)).to(torch.bfloat16)
+    q, xsc = W.quantize_rowwise(xsil)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    def gemv(i):
+        w = ws_[i % nsets]
+        W._lib.check(lib.w8a8_gemv_dequant(q.data_ptr(), w.data_ptr(), xsc.data_ptr(), wsc.data_ptr(), n,
+                                           bias.data_ptr(), out.data_ptr(), W._lib.BF16, m, n, k, 0, stream()))
+    ms = median_of_batches(gemv)
+    ex["gemv_adaln_M2_K3072_N18432"] = {"us": round(ms * 1e3, 2), "GB/s": round(per / (ms * 1e-3) / 1e9, 1),
+                                        "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+                                        "bytes": per, "buffer_sets": nsets}
+    del ws_
+    # outlier workload: fused quant+GEMM vs unfused
+    m, k, n = M_TOK, HID, FFN
+    x = student_t(m, k, 3).to(dev)
+    w, wsc, b = make_linear(k, n, 30, dev)
+    qo = torch.empty(m, k, dtype=torch.int8, device=dev)
+    so = torch.empty(m, 1, dtype=torch.float32, device=dev)
+    o = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    def unfused(i):
+        W._lib.check(lib.w8a8_quantize_rowwise(x.data_ptr(), W._lib.BF16, qo.data_ptr(), so.data_ptr(), m, k, 0, stream()))
+        W._lib.check(lib.w8a8_gemm_dequant(qo.data_ptr(), w.data_ptr(), so.data_ptr(), wsc.data_ptr(), n,
+                                           b.data_ptr(), o.data_ptr(), W._lib.BF16, m, n, k, 0, stream()))
+    def fused(i):
+        W._lib.check(lib.w8a8_row_scales(x.data_ptr(), W._lib.BF16, so.data_ptr(), m, k, 0, stream()))
+        W._lib.check(lib.w8a8_gemm_dequant_xq(x.data_ptr(), W._lib.BF16, so.data_ptr(), w.data_ptr(),
+                                              wsc.data_ptr(), n, b.data_ptr(), o.data_ptr(), W._lib.BF16,
+                                              m, n, k, 0, stream()))
+    mu = median_of_batches(unfused, warmup=5, batches=5, calls=10)
+    mf = median_of_batches(fused, warmup=5, batches=5, calls=10)
+    ops = 2 * m * n * k
+    ex["outlier_quant_gemm_11712x3072x12288"] = {
+        "unfused_us": round(mu * 1e3, 1), "fused_us": round(mf * 1e3, 1),
+        "unfused_TOPS": round(ops / (mu * 1e-3) / 1e12, 1), "fused_TOPS": round(ops / (mf * 1e-3) / 1e12, 1)}
+    return ex
+
+
+def run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs):
+    """One kernel in a loop (for rocprofv3 --pmc / --kernel-trace runs)."""
+    n_iter = max(args.steps, 1)
+    if args.only == "up_gemm":
+        quant(x_ffn, qbuf[HID])
+        for _ in range(n_iter):
+            gemm(qbuf[HID], layers[2], outs["up"], True)
+    elif args.only == "quant":
+        for _ in range(n_iter):
+            quant(x_ffn, qbuf[HID])
+    elif args.only == "step":
+        for _ in range(n_iter):
+            step()
+    else:
+        raise SystemExit(f"unknown --only {args.only}")
+    torch.cuda.synchronize()
+    print(f"[bench] ran {args.only} x{n_iter}", file=sys.stderr, flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,12 @@
+"""MI355X (gfx950) W8A8 linear family: per-token INT8 quantization, INT8 MFMA
+GEMM with fused dequant epilogue, M<=2 GEMV, behind the C ABI in include/w8a8.h.
+
+Drop-in for the reference crate's ``int8_linear`` operator
+(inference/src/cuda_linear.rs:311-317).
+"""
+from . import _lib
+from .ops import (apply_residual, dequantize_linear, gemm_dequant, gemm_dequant_xq, gemm_i32,
+                  gemv_dequant, int8_linear, quantize_rowwise, route, row_scales)
+
+__all__ = ["int8_linear", "quantize_rowwise", "row_scales", "gemv_dequant", "gemm_dequant",
+           "gemm_dequant_xq", "gemm_i32", "dequantize_linear", "apply_residual", "route", "_lib"]

@@ -1,0 +1,68 @@
+"""Build libw8a8_hip.so in-tree with hipcc for gfx950.
+
+    python -m imagine_amd.build            # or: python imagine_amd/build.py
+
+Each .hip source compiles to its own object in parallel, then one link.
+Flags: -O3, IEEE float (no fast-math; contractions only where fmaf is
+written), packed-fp32 instructions disabled.
+"""
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libw8a8_hip.so"
+SOURCES = ["w8a8_quant.hip", "w8a8_gemv.hip", "w8a8_gemm.hip", "w8a8_api.hip"]
+ARCH = os.environ.get("W8A8_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc():
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC)")
+
+
+def flags():
+    return [
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+        "-fno-fast-math", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        f"-I{ROOT / 'include'}", "-Wall", "-Wno-unused-function",
+    ]
+
+
+def build(verbose=False, extra=()):
+    cc = hipcc()
+    with tempfile.TemporaryDirectory(prefix="w8a8_build_") as tmp:
+        def compile_one(src):
+            obj = Path(tmp) / (Path(src).stem + ".o")
+            cmd = [cc, *flags(), *extra, "-c", str(CSRC / src), "-o", str(obj)]
+            r = subprocess.run(cmd, capture_output=True, text=True)
+            noise = "is not a recognized feature for this target"
+            err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+            if r.returncode != 0:
+                raise RuntimeError(f"hipcc failed for {src}:\n{err}")
+            if verbose and err.strip():
+                print(err, file=sys.stderr)
+            return obj
+
+        with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
+            objs = list(ex.map(compile_one, SOURCES))
+        tmp_lib = Path(tmp) / LIB.name
+        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp_lib)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed:\n{r.stderr}")
+        shutil.copy2(tmp_lib, LIB.with_suffix(".so.tmp"))
+        os.replace(LIB.with_suffix(".so.tmp"), LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,204 @@
+// C ABI of libw8a8_hip.so (declared in include/w8a8.h).
+//
+// Argument checks and error behaviour mirror the reference's native wrappers
+// (Kitchen dlpack_bindings.cpp:2307-2335, :2747-2763, :3485-3660) and the
+// bridge's error-code mapping (inference/native/bridge.cpp:75-81,434-439).
+// Messages of the checks the crate's callers can trigger are the reference's
+// own text, so a caller that matches on them keeps working.
+#include <cstdio>
+#include <string>
+
+#include "w8a8_common.h"
+
+namespace w8a8 {
+void launch_quantize(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M, int64_t K,
+                     bool recip, bool gelu, bool scales_only, hipStream_t stream);
+void launch_gemv(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                 int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
+                 int64_t K, bool gelu, hipStream_t stream);
+void launch_gemm(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                 int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
+                 int64_t K, bool gelu, bool int32_out, hipStream_t stream);
+bool launch_gemm_xq(const void* x, int x_dtype, const float* xs, const int8_t* w, const float* ws,
+                    int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M,
+                    int64_t N, int64_t K, bool gelu, hipStream_t stream);
+void launch_dequant(const int32_t* acc, const float* xs, const float* ws, int64_t ws_size,
+                    const void* bias, void* out, int out_dtype, int64_t M, int64_t N, bool gelu,
+                    hipStream_t stream);
+}  // namespace w8a8
+
+namespace {
+
+thread_local std::string g_last_error;
+thread_local int g_last_accel = 0;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        g_last_accel = static_cast<int>(e);
+        return fail(W8A8_ERR_ACCELERATOR, std::string(what) + ": " + hipGetErrorString(e));
+    }
+    return W8A8_OK;
+}
+
+bool valid_dtype(int d) { return d == W8A8_F32 || d == W8A8_F16 || d == W8A8_BF16; }
+
+constexpr uint32_t kKnownFlags = W8A8_SCALE_RECIP | W8A8_ACT_GELU_TANH | W8A8_OUT_INT32 |
+                                 W8A8_FUSED_QUANT | W8A8_ROUTE_GEMM;
+
+int check_common(int64_t M, int64_t N, int64_t K, uint32_t flags) {
+    if (M < 0 || N < 0 || K < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (flags & ~kKnownFlags) return fail(W8A8_ERR_VALUE, "unknown flag bits");
+    return W8A8_OK;
+}
+
+int check_ws(int64_t ws_size, int64_t N, const char* msg) {
+    if (ws_size != 1 && ws_size != N) return fail(W8A8_ERR_RUNTIME, msg);
+    return W8A8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* w8a8_last_error(void) { return g_last_error.c_str(); }
+int w8a8_last_accelerator_code(void) { return g_last_accel; }
+const char* w8a8_version(void) { return "w8a8-hip 0.1 gfx950"; }
+
+int w8a8_quantize_rowwise(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M, int64_t K,
+                          uint32_t flags, hipStream_t stream) {
+    if (int rc = check_common(M, 0, K, flags)) return rc;
+    if (!valid_dtype(x_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for INT8 quantization");
+    if (M == 0) return W8A8_OK;
+    if (K > 0 && (!x || !q)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (!xs) return fail(W8A8_ERR_VALUE, "null scale pointer");
+    w8a8::launch_quantize(x, x_dtype, q, xs, M, K, flags & W8A8_SCALE_RECIP,
+                          flags & W8A8_ACT_GELU_TANH, false, stream);
+    return check_launch("quantize_int8_rowwise");
+}
+
+int w8a8_row_scales(const void* x, int x_dtype, float* xs, int64_t M, int64_t K, uint32_t flags,
+                    hipStream_t stream) {
+    if (int rc = check_common(M, 0, K, flags)) return rc;
+    if (!valid_dtype(x_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for INT8 quantization");
+    if (M == 0) return W8A8_OK;
+    if ((K > 0 && !x) || !xs) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    w8a8::launch_quantize(x, x_dtype, nullptr, xs, M, K, flags & W8A8_SCALE_RECIP,
+                          flags & W8A8_ACT_GELU_TANH, true, stream);
+    return check_launch("row_scales");
+}
+
+int w8a8_gemv_dequant(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                      int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M,
+                      int64_t N, int64_t K, uint32_t flags, hipStream_t stream) {
+    if (int rc = check_common(M, N, K, flags)) return rc;
+    if (M != 1 && M != 2) return fail(W8A8_ERR_RUNTIME, "INT8 GEMV dequant expects M == 1 or M == 2");
+    if (!valid_dtype(out_dtype)) return fail(W8A8_ERR_RUNTIME, "Invalid INT8 GEMV output dtype code");
+    if (int rc = check_ws(ws_size, N, "INT8 GEMV weight scale must be scalar or per-output-channel")) return rc;
+    if (N == 0) return W8A8_OK;
+    if (!out || !xs || !ws || (K > 0 && (!q || !w))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    w8a8::launch_gemv(q, w, xs, ws, ws_size, bias, out, out_dtype, M, N, K,
+                      flags & W8A8_ACT_GELU_TANH, stream);
+    return check_launch("int8_gemv_dequant");
+}
+
+int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                      int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M,
+                      int64_t N, int64_t K, uint32_t flags, hipStream_t stream) {
+    if (int rc = check_common(M, N, K, flags)) return rc;
+    const bool i32 = flags & W8A8_OUT_INT32;
+    if (!i32 && !valid_dtype(out_dtype)) return fail(W8A8_ERR_RUNTIME, "Invalid INT8 linear output dtype code");
+    if (!i32) {
+        if (int rc = check_ws(ws_size, N, "INT8 weight scale must be scalar or per-output-channel")) return rc;
+    }
+    if (M == 0 || N == 0) return W8A8_OK;
+    if (!out || (K > 0 && (!q || !w)) || (!i32 && (!xs || !ws))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    w8a8::launch_gemm(q, w, xs, ws, ws_size, bias, out, i32 ? W8A8_F32 : out_dtype, M, N, K,
+                      flags & W8A8_ACT_GELU_TANH, i32, stream);
+    return check_launch("int8_gemm_dequant");
+}
+
+int w8a8_gemm_dequant_xq(const void* x, int x_dtype, const float* xs, const int8_t* w,
+                         const float* ws, int64_t ws_size, const void* bias, void* out,
+                         int out_dtype, int64_t M, int64_t N, int64_t K, uint32_t flags,
+                         hipStream_t stream) {
+    if (int rc = check_common(M, N, K, flags)) return rc;
+    if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype)) return fail(W8A8_ERR_RUNTIME, "Invalid dtype code");
+    if (flags & W8A8_OUT_INT32)
+        return fail(W8A8_ERR_VALUE, "W8A8_OUT_INT32 is not available with the fused quantizer");
+    if (int rc = check_ws(ws_size, N, "INT8 weight scale must be scalar or per-output-channel")) return rc;
+    if (M == 0 || N == 0) return W8A8_OK;
+    if (!out || !xs || !ws || (K > 0 && (!x || !w))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (!w8a8::launch_gemm_xq(x, x_dtype, xs, w, ws, ws_size, bias, out, out_dtype, M, N, K,
+                              flags & W8A8_ACT_GELU_TANH, stream))
+        return fail(W8A8_ERR_RUNTIME,
+                    "fused-quant GEMM needs a 16-bit input, K % 16 == 0 and 16-byte aligned operands");
+    return check_launch("int8_gemm_dequant_xq");
+}
+
+int w8a8_dequantize_linear(const int32_t* acc, const float* xs, const float* ws, int64_t ws_size,
+                           const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
+                           uint32_t flags, hipStream_t stream) {
+    if (int rc = check_common(M, N, 0, flags)) return rc;
+    if (!valid_dtype(out_dtype)) return fail(W8A8_ERR_RUNTIME, "Invalid INT8 linear output dtype code");
+    if (int rc = check_ws(ws_size, N, "INT8 weight scale must be scalar or per-output-channel")) return rc;
+    if (M == 0 || N == 0) return W8A8_OK;
+    if (!acc || !xs || !ws || !out) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    w8a8::launch_dequant(acc, xs, ws, ws_size, bias, out, out_dtype, M, N,
+                         flags & W8A8_ACT_GELU_TANH, stream);
+    return check_launch("dequantize_int8_linear");
+}
+
+int64_t w8a8_int8_linear_workspace_bytes(int64_t M, int64_t K) {
+    if (M < 0 || K < 0) return -1;
+    // q [M, K] int8, padded to 256 bytes, then xs [M] fp32
+    return (M * K + 255) / 256 * 256 + M * 4;
+}
+
+int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
+                     const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                     uint32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    if (int rc = check_common(M, N, K, flags)) return rc;
+    if (flags & W8A8_OUT_INT32) return fail(W8A8_ERR_VALUE, "W8A8_OUT_INT32 is a GEMM-only flag");
+    if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
+        return fail(W8A8_ERR_RUNTIME, "GEMV output requires original floating dtype contract");
+    const bool gemv = !(flags & W8A8_ROUTE_GEMM) && ((M == 1 && K % 4 == 0) || (M == 2 && K % 16 == 0));
+    if (int rc = check_ws(ws_size, N, gemv ? "INT8 GEMV weight scale must be scalar or per-output-channel"
+                                           : "INT8 weight scale must be scalar or per-output-channel"))
+        return rc;
+    if (!gemv && K % 4 != 0 && M > 0 && N > 0)
+        return fail(W8A8_ERR_RUNTIME,
+                    "INT8 GEMM not supported on this GPU for these dimensions (requires SM >= 7.5, "
+                    "and dimensions multiple of 4).");
+    if (M == 0) return W8A8_OK;
+    const int64_t need = w8a8_int8_linear_workspace_bytes(M, K);
+    if (!workspace || workspace_bytes < need)
+        return fail(W8A8_ERR_VALUE, "workspace smaller than w8a8_int8_linear_workspace_bytes(M, K)");
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return fail(W8A8_ERR_VALUE, "workspace must be 256-byte aligned");
+    int8_t* q = static_cast<int8_t*>(workspace);
+    float* xs = reinterpret_cast<float*>(static_cast<char*>(workspace) + (M * K + 255) / 256 * 256);
+    const uint32_t qflags = flags & (W8A8_SCALE_RECIP | W8A8_ACT_GELU_TANH);
+    // The input activation is applied before quantization; the GEMM/GEMV
+    // epilogue itself runs without GELU here.
+    // Fused route: row scales, then a GEMM that quantizes its activation tiles
+    // (an input activation is only applied by the standalone quantizer).
+    if (!gemv && (flags & W8A8_FUSED_QUANT) && !(qflags & W8A8_ACT_GELU_TANH) && N > 0 &&
+        x_dtype != W8A8_F32 && K % 16 == 0) {
+        if (int rc = w8a8_row_scales(x, x_dtype, xs, M, K, qflags, stream)) return rc;
+        if (w8a8::launch_gemm_xq(x, x_dtype, xs, w, ws, ws_size, bias, out, out_dtype, M, N, K,
+                                 false, stream))
+            return check_launch("int8_gemm_dequant_xq");
+    }
+    if (int rc = w8a8_quantize_rowwise(x, x_dtype, q, xs, M, K, qflags, stream)) return rc;
+    if (N == 0) return W8A8_OK;
+    if (gemv) return w8a8_gemv_dequant(q, w, xs, ws, ws_size, bias, out, out_dtype, M, N, K, 0, stream);
+    return w8a8_gemm_dequant(q, w, xs, ws, ws_size, bias, out, out_dtype, M, N, K, 0, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,175 @@
+// Shared device helpers for the gfx950 W8A8 kernels.
+//
+// All float arithmetic here is IEEE binary32 in the written order: the library
+// is compiled with -ffp-contract=off and every fused multiply-add is spelled
+// out as fmaf.  Conversions to 16-bit types round to nearest even.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/w8a8.h"
+
+namespace w8a8 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- 16-bit floats
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round to nearest even (finite inputs; NaN keeps a quiet payload).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+    // The hardware conversion (v_cvt_f16_f32) rounds to nearest even in the
+    // default mode, including subnormal results and overflow to infinity.
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <int DT> struct DType;
+template <> struct DType<W8A8_F32> {
+    using storage = float;
+    static constexpr int bytes = 4;
+    __device__ static float load(const storage v) { return v; }
+    __device__ static storage store(float f) { return f; }
+    __device__ static float round(float f) { return f; }
+    static constexpr float finite_max = 3.40282347e38f;
+    static constexpr float tiny = 1.17549435e-38f;
+};
+template <> struct DType<W8A8_F16> {
+    using storage = uint16_t;
+    static constexpr int bytes = 2;
+    __device__ static float load(const storage v) { return f16_to_f32(v); }
+    __device__ static storage store(float f) { return f32_to_f16(f); }
+    __device__ static float round(float f) { return f16_to_f32(f32_to_f16(f)); }
+    static constexpr float finite_max = 65504.0f;
+    static constexpr float tiny = 6.103515625e-5f;
+};
+template <> struct DType<W8A8_BF16> {
+    using storage = uint16_t;
+    static constexpr int bytes = 2;
+    __device__ static float load(const storage v) { return bf16_to_f32(v); }
+    __device__ static storage store(float f) { return f32_to_bf16(f); }
+    __device__ static float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+    static constexpr float finite_max = 3.38953139e38f;
+    static constexpr float tiny = 1.17549435e-38f;
+};
+
+// ---------------------------------------------------------------- GELU (tanh)
+
+// 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), ATen's operation
+// order for the tanh approximation; the reference applies it as input_act
+// "gelu_tanh" (inference/src/int8_linear.rs:37-41).
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float kBeta = 0.79788456080286535588f;  // sqrt(2) * (2/sqrt(pi)) * 0.5
+    const float kKappa = 0.044715f;
+    float x_cube = x * x * x;
+    float inner = kBeta * (x + kKappa * x_cube);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+// ---------------------------------------------------------------- quantizer math
+
+// Row scale from the row's absolute maximum.
+//   IEEE form:  max(amax / 127, 1e-30)                 (eager.rs:159-165)
+//   RECIP form: max(min(amax, T_max) * (1/127), 1e-30) (int8_linear.cu:36-39,205-208)
+template <int DT>
+__device__ __forceinline__ float row_scale(float amax, bool recip) {
+    float s;
+    if (recip) {
+        s = fminf(amax, DType<DT>::finite_max) * (1.0f / 127.0f);
+    } else {
+        s = amax / 127.0f;  // correctly rounded: no fast-math in this library
+    }
+    return fmaxf(s, 1.0e-30f);
+}
+
+// Per-row constants of the element quantizer: the divisor sT = T(s) (zero
+// replaced by T's tiny, eager.rs:94-109) and its correctly rounded reciprocal.
+struct RowQuant {
+    float d;  // sT
+    float r;  // RN(1 / sT)
+};
+
+template <int DT>
+__device__ __forceinline__ RowQuant row_quant(float s) {
+    RowQuant rq;
+    float d = DType<DT>::round(s);
+    if (d == 0.0f) d = DType<DT>::tiny;
+    rq.d = d;
+    rq.r = 1.0f / d;
+    return rq;
+}
+
+// RN(x / d) from the reciprocal: q0 = RN(x * r), remainder e = x - q0*d
+// (exact in one fma), corrected quotient RN(q0 + e * r).  With r = RN(1/d)
+// this is the correctly rounded quotient; that is verified exhaustively for
+// every bf16 and fp16 (x, d) pair a row can produce (tests/test_divide.py).
+// fp32 inputs use the hardware's IEEE division instead.
+__device__ __forceinline__ float div_rn(float x, const RowQuant& rq) {
+    float q0 = x * rq.r;
+    float e = fmaf(-q0, rq.d, x);
+    return fmaf(e, rq.r, q0);
+}
+
+// One element: q = clamp(rint(T(x / sT)), -128, 127) as int.
+template <int DT>
+__device__ __forceinline__ int quant_elem(float x, const RowQuant& rq) {
+    float quot;
+    if constexpr (DT == W8A8_F32) {
+        quot = x / rq.d;
+    } else {
+        quot = DType<DT>::round(div_rn(x, rq));
+    }
+    float v = __builtin_rintf(quot);
+    v = fminf(fmaxf(v, -128.0f), 127.0f);
+    return static_cast<int>(v);
+}
+
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
+    return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
+           ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);
+}
+
+// ---------------------------------------------------------------- epilogue
+
+// out = O( fma(float(acc) * xs, ws, bias) ), optional gelu on the O-rounded value.
+template <int ODT>
+__device__ __forceinline__ float epilogue_value(int acc, float xs, float ws, float bias, bool gelu) {
+    float t = static_cast<float>(acc) * xs;
+    float v = fmaf(t, ws, bias);
+    if (gelu) v = gelu_tanh(DType<ODT>::round(v));
+    return v;
+}
+
+// ---------------------------------------------------------------- wave reductions
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+}  // namespace w8a8

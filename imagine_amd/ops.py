@@ -1,0 +1,247 @@
+"""Torch-facing W8A8 operators over the C ABI (device memory and streams only).
+
+``int8_linear`` mirrors the reference crate's operator: its kwargs, route
+selection, argument conversions and error classes/messages follow
+``inference/src/cuda_linear.rs:311-317,419-824`` (with the signature at
+``inference/src/backend_signatures.rs:445-460``).  The arithmetic runs in the
+HIP kernels of libw8a8_hip.so; torch only allocates tensors, converts dtypes
+of small operands (scales, bias) and supplies the current stream.
+
+Not built here (raise NotImplementedError): ConvRot rotation, and the
+SwiGLU / SiTU / RMSNorm input activations.
+"""
+import torch
+
+from . import _lib
+
+_CODE = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dtype_code(dtype, what):
+    if dtype not in _CODE:
+        raise RuntimeError(f"{what} requires original floating dtype contract")
+    return _CODE[dtype]
+
+
+def _require_cuda(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError("W8A8 HIP path requires device tensors on a ROCm GPU")
+
+
+def _as_2d(x):
+    if x.dim() == 2 and x.is_contiguous():
+        return x
+    if x.dim() == 0:
+        raise IndexError("tuple index out of range")
+    return x.reshape(-1, x.shape[-1]).contiguous()
+
+
+def _weight_scale(ws, device):
+    """cuda_linear.rs:530-540: fp32, contiguous, flattened, on the device."""
+    if ws.device == device and ws.dtype == torch.float32 and ws.is_contiguous():
+        return ws.reshape(-1)
+    return ws.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+
+
+def _bias(bias, device, dtype):
+    """cuda_linear.rs:26-51,541-551: output dtype, contiguous, 16-byte aligned."""
+    if bias is None:
+        return None
+    b = bias
+    if b.device != device or b.dtype != dtype or not b.is_contiguous():
+        b = b.to(device=device, dtype=dtype).contiguous()
+    if b.data_ptr() % 16 != 0:
+        b = b.clone()
+    return b
+
+
+# ---------------------------------------------------------------- primitives
+
+
+def quantize_rowwise(x, scale_form="ieee", input_act=None):
+    """Per-token quantization of a [M, K] device tensor -> (q int8 [M, K], s fp32 [M, 1]).
+
+    The reference's ``quantize_int8_rowwise`` (int8_linear.cu:1322-1371).
+    ``scale_form`` "ieee" (amax / 127, the reference CPU route) or "recip"
+    (amax * (1/127), the reference CUDA kernel)."""
+    _require_cuda(x)
+    x = _as_2d(x)
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    flags = (_lib.SCALE_RECIP if scale_form == "recip" else 0) | (
+        _lib.ACT_GELU_TANH if input_act == "gelu_tanh" else 0)
+    _lib.check(_lib.load().w8a8_quantize_rowwise(
+        _ptr(x), _dtype_code(x.dtype, "INT8 quantization"), _ptr(q), _ptr(s), M, K, flags,
+        _stream(x.device)))
+    return q, s
+
+
+def row_scales(x, scale_form="ieee"):
+    """Row scales only (fp32 [M, 1]); the first pass of the fused quant+GEMM."""
+    _require_cuda(x)
+    x = _as_2d(x)
+    M, K = x.shape
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    flags = _lib.SCALE_RECIP if scale_form == "recip" else 0
+    _lib.check(_lib.load().w8a8_row_scales(_ptr(x), _dtype_code(x.dtype, "INT8 quantization"),
+                                           _ptr(s), M, K, flags, _stream(x.device)))
+    return s
+
+
+def gemv_dequant(q, w, xs, ws, bias, out_dtype, gelu=False):
+    """M = 1 / 2 GEMV + dequant (the reference's ``int8_gemv_dequant``)."""
+    _require_cuda(q, w, xs, ws, bias)
+    M, K = q.shape
+    N = w.shape[0]
+    out = torch.empty((M, N), dtype=out_dtype, device=q.device)
+    _lib.check(_lib.load().w8a8_gemv_dequant(
+        _ptr(q), _ptr(w), _ptr(xs), _ptr(ws), ws.numel(), _ptr(bias), _ptr(out),
+        _dtype_code(out_dtype, "GEMV output"), M, N, K,
+        _lib.ACT_GELU_TANH if gelu else 0, _stream(q.device)))
+    return out
+
+
+def gemm_dequant(q, w, xs, ws, bias, out_dtype, gelu=False, out=None):
+    """INT8 GEMM + fused dequant epilogue (the reference's ``cutlass_int8_dequant``)."""
+    _require_cuda(q, w, xs, ws, bias)
+    M, K = q.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=q.device)
+    _lib.check(_lib.load().w8a8_gemm_dequant(
+        _ptr(q), _ptr(w), _ptr(xs), _ptr(ws), ws.numel(), _ptr(bias), _ptr(out),
+        _dtype_code(out_dtype, "INT8 linear output"), M, N, K,
+        _lib.ACT_GELU_TANH if gelu else 0, _stream(q.device)))
+    return out
+
+
+def gemm_i32(q, w, out=None):
+    """INT8 GEMM with int32 output (the reference's ``cublas_gemm_int8``)."""
+    _require_cuda(q, w)
+    M, K = q.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.int32, device=q.device)
+    _lib.check(_lib.load().w8a8_gemm_dequant(
+        _ptr(q), _ptr(w), None, None, 1, None, _ptr(out), _lib.F32, M, N, K, _lib.OUT_INT32,
+        _stream(q.device)))
+    return out
+
+
+def gemm_dequant_xq(x, xs, w, ws, bias, out_dtype, gelu=False, out=None):
+    """GEMM that quantizes the 16-bit activation ``x`` inside its tile loads,
+    given the row scales ``xs`` from :func:`row_scales`."""
+    _require_cuda(x, xs, w, ws, bias)
+    M, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    _lib.check(_lib.load().w8a8_gemm_dequant_xq(
+        _ptr(x), _dtype_code(x.dtype, "INT8 quantization"), _ptr(xs), _ptr(w), _ptr(ws), ws.numel(),
+        _ptr(bias), _ptr(out), _dtype_code(out_dtype, "INT8 linear output"), M, N, K,
+        _lib.ACT_GELU_TANH if gelu else 0, _stream(x.device)))
+    return out
+
+
+def dequantize_linear(acc, xs, ws, bias, out_dtype, gelu=False):
+    """Standalone int32 -> out dequant (the reference's ``dequantize_int8_linear``)."""
+    _require_cuda(acc, xs, ws, bias)
+    M, N = acc.shape
+    out = torch.empty((M, N), dtype=out_dtype, device=acc.device)
+    _lib.check(_lib.load().w8a8_dequantize_linear(
+        _ptr(acc), _ptr(xs), _ptr(ws), ws.numel(), _ptr(bias), _ptr(out),
+        _dtype_code(out_dtype, "INT8 linear output"), M, N, _lib.ACT_GELU_TANH if gelu else 0,
+        _stream(acc.device)))
+    return out
+
+
+# ---------------------------------------------------------------- operator
+
+
+def route(m, k, n):
+    """The reference's route choice (cuda_linear.rs:498-511, :836-860), non-ConvRot.
+
+    Returns "m1", "gemv" or "gemm".  The M=1 route is a quantize + GEMV pair in
+    the reference too (Kitchen int8_linear_m1, dlpack_bindings.cpp:3594-3660),
+    so "m1" and "gemv" run the same kernels here."""
+    if m == 1 and k % 4 == 0 and (k <= 2560 or (k == 6144 and n <= 128)):
+        return "m1"
+    if (m == 1 and k % 4 == 0) or (m == 2 and k % 16 == 0):
+        return "gemv"
+    return "gemm"
+
+
+def apply_residual(out, residual, scale):
+    """int8_linear.rs:99-111: residual.to(out).addcmul(out, scale.to(out))."""
+    if residual is None:
+        return out
+    if scale is None:
+        raise ValueError("residual requires residual_scale")
+    return residual.to(out.dtype).addcmul(out, scale.to(out.dtype))
+
+
+def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=False,
+                convrot_groupsize=256, input_act=None, input_act_weight=None, input_act_eps=None,
+                residual=None, residual_scale=None, *, scale_form="ieee", fused_quant=False,
+                workspace=None):
+    """W8A8 linear: quantize x per token, INT8 GEMM/GEMV, dequant to ``out_dtype``.
+
+    Same keyword arguments, in the same order, as the crate's
+    ``("cuda", "int8_linear")`` operator (backend_signatures.rs:445-460).
+    Extra keyword-only knobs: ``scale_form`` ("ieee" default, or "recip"),
+    ``fused_quant`` (quantize inside the GEMM's tile loads), ``workspace`` (a
+    preallocated uint8 device buffer of at least
+    ``w8a8_int8_linear_workspace_bytes(M, K)`` bytes, 256-byte aligned).
+    """
+    if residual is not None and residual_scale is None:
+        raise ValueError("int8_linear: residual requires residual_scale")
+    if convrot:
+        raise NotImplementedError("ConvRot activation rotation is not part of this build")
+    if input_act not in (None, "gelu_tanh"):
+        raise NotImplementedError(f"input_act {input_act!r} is not part of this build")
+    _require_cuda(x, weight)
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    shape = x.shape
+    x2 = _as_2d(x)
+    weight = weight.contiguous()
+    m, k = x2.shape
+    n, kw = weight.shape
+    if k != kw:
+        raise AssertionError("Input and weight inner dimensions must match")
+    out_code = _dtype_code(out_dtype, "GEMV output")
+    r = route(m, k, n)
+    ws = _weight_scale(weight_scale, x.device)
+    if ws.numel() not in (1, n):
+        if r == "gemm":
+            ws.expand([n])  # raises the reference's torch expand error (cuda_linear.rs:702-706)
+        raise RuntimeError("INT8 GEMV weight scale must be scalar or per-output-channel")
+    if r == "gemv" and m == 2 and weight.data_ptr() % 16 != 0:
+        weight = weight.clone()  # cuda_linear.rs:623-625
+    b = _bias(bias, x.device, out_dtype)
+    out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    lib = _lib.load()
+    need = lib.w8a8_int8_linear_workspace_bytes(m, k)
+    if workspace is None or workspace.numel() < need or workspace.data_ptr() % 256 != 0:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    flags = (_lib.SCALE_RECIP if scale_form == "recip" else 0) | (
+        _lib.ACT_GELU_TANH if input_act == "gelu_tanh" else 0) | (
+        _lib.FUSED_QUANT if fused_quant else 0)
+    _lib.check(lib.w8a8_int8_linear(
+        _ptr(x2), _dtype_code(x2.dtype, "INT8 quantization"), _ptr(weight), _ptr(ws), ws.numel(),
+        _ptr(b), _ptr(out), out_code, m, n, k, flags, _ptr(workspace), workspace.numel(),
+        _stream(x.device)))
+    if residual is not None:
+        out = apply_residual(out, residual.reshape(out.shape), residual_scale)
+    if len(shape) == 2:
+        return out
+    return out.reshape(*shape[:-1], n)

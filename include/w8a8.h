@@ -1,0 +1,132 @@
+/*
+ * w8a8.h -- C ABI of libw8a8_hip.so, the MI355X (gfx950) W8A8 linear family.
+ *
+ * Drop-in replacement for the native calls the reference crate's int8_linear
+ * operator makes through its C bridge (inference/native/bridge.hpp:29,
+ * inference/native/bridge.cpp:415-440 -> Kitchen launchers).  Every entry point
+ * takes plain device pointers, sizes, dtype codes and a HIP stream; nothing
+ * is allocated or freed inside, nothing synchronizes (the reference's contract:
+ * cuda_linear.rs:603-604,638,681,767 preallocate every output; bridge.cpp
+ * launches on the caller's stream).
+ *
+ * Layouts (all row-major, contiguous):
+ *   x       [M, K]   fp32 / fp16 / bf16 activations
+ *   q       [M, K]   int8 quantized activations
+ *   xs      [M]      fp32 per-row (per-token) scales     (the reference's [M,1])
+ *   w       [N, K]   int8 weights, one row per output channel
+ *   ws      [N] or [1] fp32 per-output-channel (or scalar) weight scales
+ *   bias    [N]      in the output dtype, or NULL
+ *   out     [M, N]   fp32 / fp16 / bf16
+ *
+ * Return codes follow the reference bridge (bridge.cpp:75-81,434-439):
+ *   0 ok, -1 runtime error, -9 out of memory, -10 accelerator error
+ *   (code in w8a8_last_accelerator_code()), -20 ValueError, -21 IndexError.
+ * The message of the last failure on the calling thread is w8a8_last_error().
+ */
+#ifndef W8A8_H
+#define W8A8_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes: the reference's output codes (cuda_linear.rs:488-497). */
+#define W8A8_F32 0
+#define W8A8_F16 1
+#define W8A8_BF16 2
+
+#define W8A8_OK 0
+#define W8A8_ERR_RUNTIME (-1)
+#define W8A8_ERR_OOM (-9)
+#define W8A8_ERR_ACCELERATOR (-10)
+#define W8A8_ERR_VALUE (-20)
+#define W8A8_ERR_INDEX (-21)
+
+/* flags */
+#define W8A8_SCALE_RECIP (1u << 0)   /* scale = amax * (1/127f), the reference's CUDA
+                                        kernel form (int8_linear.cu:205-208); default is
+                                        IEEE amax / 127, its CPU form (eager.rs:159-165) */
+#define W8A8_ACT_GELU_TANH (1u << 1) /* quantize: gelu_tanh on x first (input_act,
+                                        int8_linear.rs:37-41); GEMM/GEMV/dequant:
+                                        gelu_tanh on the output-dtype value */
+#define W8A8_OUT_INT32 (1u << 2)     /* GEMM: store the int32 accumulators (out is int32) */
+#define W8A8_FUSED_QUANT (1u << 3)   /* w8a8_int8_linear: GEMM route quantizes x inside
+                                        the GEMM's activation-tile load */
+#define W8A8_ROUTE_GEMM (1u << 4)    /* w8a8_int8_linear: skip the M<=2 GEMV routes */
+
+const char* w8a8_last_error(void);
+int w8a8_last_accelerator_code(void);
+/* Library version string ("w8a8-hip <major>.<minor> gfx950"). */
+const char* w8a8_version(void);
+
+/* Per-token dynamic absmax INT8 quantization.
+ * Replaces Kitchen `quantize_int8_rowwise` (int8_linear.cu:184-227, launcher
+ * :1322-1371), called by the crate at cuda_linear.rs:600-619.
+ *   s[m] = max(amax_m / 127, 1e-30)
+ *   q[m,k] = clamp(rint(T(x[m,k] / T(s[m]))), -128, 127)
+ * Flags: W8A8_SCALE_RECIP, W8A8_ACT_GELU_TANH. */
+int w8a8_quantize_rowwise(const void* x, int x_dtype, int8_t* q, float* xs,
+                          int64_t M, int64_t K, uint32_t flags, hipStream_t stream);
+
+/* Row scales only (pass 1 of the fused quant+GEMM): xs[m] as above. */
+int w8a8_row_scales(const void* x, int x_dtype, float* xs, int64_t M, int64_t K,
+                    uint32_t flags, hipStream_t stream);
+
+/* M = 1 or 2 GEMV with the dequant epilogue.
+ * Replaces Kitchen `int8_gemv_dequant` (dlpack_bindings.cpp:3535-3592;
+ * int8_linear.cu:628-708, launcher :1800-1854), called at cuda_linear.rs:622-679:
+ *   out[m,n] = O(fma(float(sum_k q[m,k] w[n,k]) * xs[m], ws[n], bias[n]))
+ * ws_size is 1 or N.  Flags: W8A8_ACT_GELU_TANH. */
+int w8a8_gemv_dequant(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                      int64_t ws_size, const void* bias, void* out, int out_dtype,
+                      int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream);
+
+/* INT8 GEMM with the fused dequant epilogue (MFMA, gfx950).
+ * Replaces Kitchen `cutlass_int8_dequant` (cutlass_gemm_int8.cu:63-120,373-388),
+ * called at cuda_linear.rs:745-763, and, with W8A8_OUT_INT32, `cublas_gemm_int8`
+ * (cublas_gemm_int8.cu:176-221, called at cuda_linear.rs:765-779):
+ *   out[m,n] = O(fma(float(sum_k q[m,k] w[n,k]) * xs[m], ws[n], bias[n]))
+ * Flags: W8A8_ACT_GELU_TANH, W8A8_OUT_INT32 (xs, ws, bias ignored). */
+int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                      int64_t ws_size, const void* bias, void* out, int out_dtype,
+                      int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream);
+
+/* GEMM that quantizes the activation inside its tile load: x is the float
+ * activation and xs its row scales from w8a8_row_scales (same flags).  Output
+ * is bit-identical to w8a8_quantize_rowwise followed by w8a8_gemm_dequant.
+ * No reference counterpart as one call: it fuses quantize_int8_rowwise
+ * (int8_linear.cu:184-227) into cutlass_int8_dequant (cutlass_gemm_int8.cu:373-388). */
+int w8a8_gemm_dequant_xq(const void* x, int x_dtype, const float* xs, const int8_t* w,
+                         const float* ws, int64_t ws_size, const void* bias, void* out,
+                         int out_dtype, int64_t M, int64_t N, int64_t K, uint32_t flags,
+                         hipStream_t stream);
+
+/* Standalone dequant of int32 accumulators.
+ * Replaces Kitchen `dequantize_int8_linear` (int8_linear.cu:517-583, launcher
+ * :1721-1798), called at cuda_linear.rs:783-794. */
+int w8a8_dequantize_linear(const int32_t* acc, const float* xs, const float* ws,
+                           int64_t ws_size, const void* bias, void* out, int out_dtype,
+                           int64_t M, int64_t N, uint32_t flags, hipStream_t stream);
+
+/* Operator-level W8A8 linear: the crate's int8_dispatch without ConvRot and
+ * residual (cuda_linear.rs:419-824): quantize, then the GEMV route for
+ * (M == 1 && K % 4 == 0) || (M == 2 && K % 16 == 0) (:498-511, :836-860),
+ * else the GEMM route (which, like the reference's, needs K % 4 == 0).
+ * The caller provides the workspace for q and xs (the crate allocates them per
+ * call, :603-604); w8a8_int8_linear_workspace_bytes gives its size.
+ * Flags: W8A8_SCALE_RECIP, W8A8_ACT_GELU_TANH (applied to x, as input_act),
+ * W8A8_FUSED_QUANT, W8A8_ROUTE_GEMM. */
+int64_t w8a8_int8_linear_workspace_bytes(int64_t M, int64_t K);
+int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* ws,
+                     int64_t ws_size, const void* bias, void* out, int out_dtype,
+                     int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W8A8_H */

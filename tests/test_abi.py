@@ -1,0 +1,91 @@
+"""The C-ABI library loads, exports every symbol include/w8a8.h declares, and
+rejects invalid arguments before touching the GPU (no device needed)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from imagine_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "w8a8.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(w8a8_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_workspace_size():
+    lib = _lib.load()
+    assert b"gfx950" in lib.w8a8_version()
+    assert lib.w8a8_int8_linear_workspace_bytes(11712, 3072) == 11712 * 3072 + 4 * 11712
+    assert lib.w8a8_int8_linear_workspace_bytes(3, 5) == 256 + 12
+    assert lib.w8a8_int8_linear_workspace_bytes(-1, 5) == -1
+
+
+def _err(rc):
+    return rc, _lib.load().w8a8_last_error().decode()
+
+
+def test_argument_errors_return_reference_codes_and_messages():
+    lib = _lib.load()
+    # negative dimension -> ValueError code
+    assert _err(lib.w8a8_quantize_rowwise(None, 2, None, None, -1, 4, 0, None))[0] == _lib.ERR_VALUE
+    # unknown flag bits
+    assert _err(lib.w8a8_quantize_rowwise(None, 2, None, None, 1, 4, 1 << 30, None))[0] == _lib.ERR_VALUE
+    # bad dtype code
+    rc, msg = _err(lib.w8a8_quantize_rowwise(None, 7, None, None, 1, 4, 0, None))
+    assert rc == _lib.ERR_RUNTIME and "dtype" in msg
+    # GEMV: M must be 1 or 2 (dlpack_bindings.cpp:3545-3547)
+    rc, msg = _err(lib.w8a8_gemv_dequant(None, None, None, None, 1, None, None, 2, 3, 4, 16, 0, None))
+    assert rc == _lib.ERR_RUNTIME and msg == "INT8 GEMV dequant expects M == 1 or M == 2"
+    # GEMV: weight scale size
+    rc, msg = _err(lib.w8a8_gemv_dequant(None, None, None, None, 3, None, None, 2, 2, 4, 16, 0, None))
+    assert msg == "INT8 GEMV weight scale must be scalar or per-output-channel"
+    # operator: GEMM route needs K % 4 == 0 (cublas_gemm_int8.cu:161)
+    rc, msg = _err(lib.w8a8_int8_linear(None, 2, None, None, 1, None, None, 2, 4, 16, 15, 0, None, 0, None))
+    assert rc == _lib.ERR_RUNTIME and msg.startswith("INT8 GEMM not supported on this GPU")
+    # operator: workspace too small
+    rc, msg = _err(lib.w8a8_int8_linear(None, 2, None, None, 1, None, None, 2, 4, 16, 64, 0, None, 10, None))
+    assert rc == _lib.ERR_VALUE and "workspace" in msg
+    # empty outputs are a no-op success, nothing launched
+    assert lib.w8a8_gemm_dequant(None, None, None, None, 1, None, None, 2, 0, 16, 64, 0, None) == 0
+    assert lib.w8a8_quantize_rowwise(None, 2, None, None, 0, 64, 0, None) == 0
+
+
+def test_check_maps_codes_to_reference_exception_classes():
+    lib = _lib.load()
+    lib.w8a8_quantize_rowwise(None, 2, None, None, -1, 4, 0, None)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_VALUE)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.ERR_RUNTIME)
+    with pytest.raises(IndexError):
+        _lib.check(_lib.ERR_INDEX)
+
+
+def test_route_selection_matches_reference_selectors():
+    """cuda_int8_m1_selection fixtures + the GEMV/GEMM predicates."""
+    from imagine_amd.ops import route
+    from tests.golden import fixtures as FX
+    for c in FX.load()["cuda_int8_m1_selection"]:
+        if c["convrot"]:
+            continue
+        m, k = c["shape"][0], c["shape"][-1]
+        assert (route(m, k, c["n"]) == "m1") == c["native_m1_called"], c
+    assert route(2, 3072, 18432) == "gemv"
+    assert route(1, 2564, 4) == "gemv"
+    assert route(2, 20, 16) == "gemm"
+    assert route(11712, 3072, 12288) == "gemm"

@@ -1,0 +1,344 @@
+"""GPU parity: every HIP kernel against the oracle on identical seeded inputs.
+
+Bar: int8 codes, row scales and int32 accumulators bit-exact; epilogue
+outputs bit-exact against the oracle's single-rounding form (the same formula
+the reference's CUDA routes use); GELU outputs within one output ulp plus an
+absolute 2^-22 (libm tanhf vs the device tanhf).  Also runs the reference's
+own CUDA golden payloads through the operator.
+"""
+import numpy as np
+import pytest
+import torch
+
+import imagine_amd as W
+from oracle import oracle as O
+from tests.golden import fixtures as FX
+from tests.golden import operands as OP
+
+pytestmark = pytest.mark.gpu
+
+TD = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    W._lib.load()
+    yield
+    torch.cuda.synchronize()
+
+
+def storage(t, dtype):
+    """Host numpy storage of a tensor in oracle convention."""
+    t = t.detach().cpu().contiguous()
+    if dtype == "f32":
+        return t.numpy()
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def from_storage(a, dtype, device=DEV):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype != "f32":
+        t = t.view(torch.int16).view(TD[dtype])
+    return t.to(device)
+
+
+def make_x(m, k, dtype, seed, dist="normal"):
+    g = torch.Generator().manual_seed(seed)
+    if dist == "normal":
+        x = torch.randn(m, k, generator=g)
+    else:  # Student-t(3) with 0.1% of channels x50
+        z = torch.randn(m, k, generator=g)
+        chi = torch.randn(m, k, 3, generator=g).pow(2).sum(-1)
+        x = z / torch.sqrt(chi / 3.0)
+        idx = torch.randperm(k, generator=g)[: max(1, k // 1000)]
+        x[:, idx] *= 50.0
+    if m > 3:
+        x[3] = 0.0
+    return x.to(TD[dtype])
+
+
+def make_w(n, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+
+
+def ulp_close(got, want, dtype, abs_floor=0.0):
+    a = O.to_f32(got, dtype).astype(np.float64)
+    b = O.to_f32(want, dtype).astype(np.float64)
+    rel = {"bf16": 2.0**-7, "f16": 2.0**-10, "f32": 2.0**-23}[dtype]
+    return np.abs(a - b) <= np.abs(b) * rel + abs_floor
+
+
+# ---------------------------------------------------------------- quantizer
+
+QUANT_SHAPES = [(1, 64), (2, 3072), (7, 3072), (256, 3072), (33, 12288), (5, 1001), (3, 20000),
+                (9, 4096), (6, 9216), (4, 16)]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("shape", QUANT_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("form", ["ieee", "recip"])
+def test_quantize_bit_exact(dtype, shape, form):
+    m, k = shape
+    x = make_x(m, k, dtype, seed=m * 31 + k, dist="student_t" if k == 12288 else "normal")
+    q, s = W.quantize_rowwise(x.to(DEV), scale_form=form)
+    q_ref, s_ref = O.quant_rowwise(storage(x, dtype), dtype, scale_mode=1 if form == "recip" else 0)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+
+
+def test_quantize_unaligned_input_takes_generic_path():
+    x = make_x(5, 3073, "bf16", seed=1)
+    xd = x.to(DEV)[:, 1:]  # row stride 3073, start not 16-byte aligned
+    xc = xd.contiguous()
+    base = torch.empty(xc.numel() + 1, dtype=torch.bfloat16, device=DEV)
+    xu = base[1:].view(5, 3072)
+    xu.copy_(xc)
+    assert xu.data_ptr() % 16 != 0
+    q, s = W.quantize_rowwise(xu)
+    q_ref, s_ref = O.quant_rowwise(storage(xc, "bf16"), "bf16")
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().reshape(-1), s_ref)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_quantize_gelu_input_act(dtype):
+    x = make_x(64, 3072, dtype, seed=4)
+    q, s = W.quantize_rowwise(x.to(DEV), input_act="gelu_tanh")
+    q_ref, s_ref = O.quant_rowwise(storage(x, dtype), dtype, act=1)
+    qd = q.cpu().numpy().astype(np.int32) - q_ref.astype(np.int32)
+    assert np.abs(qd).max() <= 1 and (qd != 0).mean() < 1e-3
+    sd = np.abs(s.cpu().numpy().reshape(-1) / s_ref - 1)
+    assert sd.max() <= 2.0**-7
+
+
+def test_row_scales_equal_quantizer_scales():
+    x = make_x(100, 3072, "bf16", seed=9).to(DEV)
+    _, s = W.quantize_rowwise(x)
+    s2 = W.row_scales(x)
+    assert torch.equal(s, s2)
+
+
+def test_quantize_full_size_outlier_config_bit_exact():
+    """M=11712, K=3072, Student-t(3) with 0.1% channels x50: every code and scale."""
+    x = make_x(11712, 3072, "bf16", seed=3, dist="student_t")
+    q, s = W.quantize_rowwise(x.to(DEV))
+    q_ref, s_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+
+
+# ---------------------------------------------------------------- GEMM
+
+GEMM_SHAPES = [(256, 3072, 3072), (300, 200, 160), (1, 16, 16), (513, 257, 64), (64, 96, 48),
+               (2, 2, 32), (4, 16, 20), (7, 9, 13), (257, 512, 1024), (37, 1000, 3072)]
+
+
+@pytest.mark.parametrize("shape", GEMM_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_gemm_int32_accumulators_bit_exact(shape):
+    m, n, k = shape
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8)
+    b = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    c = W.gemm_i32(a.to(DEV), b.to(DEV))
+    assert np.array_equal(c.cpu().numpy(), O.gemm_i32(a.numpy(), b.numpy()))
+
+
+def test_gemm_int32_extremes_and_unaligned_operand():
+    m, n, k = 64, 64, 3072
+    a = torch.full((m, k), -128, dtype=torch.int8)
+    b = torch.full((n, k), -128, dtype=torch.int8)
+    c = W.gemm_i32(a.to(DEV), b.to(DEV))
+    assert (c.cpu() == k * 128 * 128).all()
+    g = torch.Generator().manual_seed(2)
+    a = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8)
+    base = torch.empty(m * k + 3, dtype=torch.int8, device=DEV)
+    au = base[3:].view(m, k)
+    au.copy_(a.to(DEV))
+    c = W.gemm_i32(au, b.to(DEV))
+    assert np.array_equal(c.cpu().numpy(), O.gemm_i32(a.numpy(), b.numpy()))
+
+
+@pytest.mark.parametrize("odt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("with_bias", [True, False])
+@pytest.mark.parametrize("ws_scalar", [False, True])
+def test_gemm_dequant_epilogue_bit_exact(odt, with_bias, ws_scalar):
+    m, n, k = 300, 520, 1024
+    x = make_x(m, k, "bf16", seed=5)
+    q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    w = make_w(n, k, seed=6)
+    g = torch.Generator().manual_seed(7)
+    ws = (torch.rand(1 if ws_scalar else n, generator=g) * 9e-3 + 1e-3).float()
+    bias = (torch.randn(n, generator=g) * 0.02).to(TD[odt]) if with_bias else None
+    out = W.gemm_dequant(torch.from_numpy(q_ref).to(DEV), w.to(DEV),
+                         torch.from_numpy(xs_ref).to(DEV), ws.to(DEV),
+                         None if bias is None else bias.to(DEV), TD[odt])
+    want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(),
+                              None if bias is None else storage(bias, odt), odt)
+    assert np.array_equal(storage(out, odt), want)
+
+
+@pytest.mark.parametrize("odt", ["bf16", "f16"])
+def test_gemm_gelu_epilogue_within_one_ulp(odt):
+    m, n, k = 260, 384, 768
+    x = make_x(m, k, "bf16", seed=8)
+    q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    w = make_w(n, k, seed=9)
+    ws = torch.full((n,), 0.004)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(1)) * 0.02).to(TD[odt])
+    out = W.gemm_dequant(torch.from_numpy(q_ref).to(DEV), w.to(DEV), torch.from_numpy(xs_ref).to(DEV),
+                         ws.to(DEV), bias.to(DEV), TD[odt], gelu=True)
+    want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt),
+                              odt, act=1)
+    got = storage(out, odt)
+    assert ulp_close(got, want, odt, abs_floor=2.0**-22).all()
+    assert (got == want).mean() > 0.999
+
+
+def test_gemm_full_size_sampled_rows_bit_exact():
+    """11712 x 3072 x 12288 (the FFN-up shape): int32 accumulators and bf16
+    outputs of 48 sampled rows against the oracle, whole output finite."""
+    m, k, n = 11712, 3072, 12288
+    x = make_x(m, k, "bf16", seed=2)
+    w = make_w(n, k, seed=3)
+    ws = (torch.rand(n, generator=torch.Generator().manual_seed(4)) * 9e-3 + 1e-3).float()
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(5)) * 0.02).to(torch.bfloat16)
+    xd, wd = x.to(DEV), w.to(DEV)
+    q, xs = W.quantize_rowwise(xd)
+    acc = W.gemm_i32(q, wd)
+    out = W.gemm_dequant(q, wd, xs, ws.to(DEV), bias.to(DEV), torch.bfloat16)
+    rows = np.sort(np.random.default_rng(0).choice(m, 48, replace=False))
+    rows[-1] = m - 1  # last (ragged) tile
+    q_ref, xs_ref = O.quant_rowwise(storage(x[rows], "bf16"), "bf16")
+    acc_ref = O.gemm_i32(q_ref, w.numpy())
+    assert np.array_equal(acc.cpu().numpy()[rows], acc_ref)
+    want = O.epilogue_kitchen(acc_ref, xs_ref, ws.numpy(), storage(bias, "bf16"), "bf16")
+    assert np.array_equal(storage(out, "bf16")[rows], want)
+    assert torch.isfinite(out.float()).all()
+
+
+# ---------------------------------------------------------------- GEMV
+
+GEMV_SHAPES = [(2, 18432, 3072), (1, 4, 3072), (2, 17, 16), (1, 129, 6144), (2, 4, 2560),
+               (1, 33, 20), (2, 5, 64), (2, 300, 12288), (1, 64, 2564)]
+
+
+@pytest.mark.parametrize("shape", GEMV_SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("odt", ["bf16", "f32"])
+def test_gemv_bit_exact(shape, odt):
+    m, n, k = shape
+    x = make_x(m, k, "bf16", seed=n + k)
+    q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    w = make_w(n, k, seed=n)
+    ws = (torch.rand(n, generator=torch.Generator().manual_seed(k)) * 9e-3 + 1e-3).float()
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(3)) * 0.02).to(TD[odt])
+    out = W.gemv_dequant(torch.from_numpy(q_ref).to(DEV), w.to(DEV), torch.from_numpy(xs_ref).to(DEV),
+                         ws.to(DEV), bias.to(DEV), TD[odt])
+    want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt), odt)
+    assert np.array_equal(storage(out, odt), want)
+
+
+def test_gemv_unaligned_weight():
+    m, n, k = 2, 40, 3072
+    x = make_x(m, k, "bf16", seed=1)
+    q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    w = make_w(n, k, seed=2)
+    base = torch.empty(n * k + 1, dtype=torch.int8, device=DEV)
+    wu = base[1:].view(n, k)
+    wu.copy_(w.to(DEV))
+    ws = torch.full((1,), 0.03125, device=DEV)
+    out = W.gemv_dequant(torch.from_numpy(q_ref).to(DEV), wu, torch.from_numpy(xs_ref).to(DEV), ws,
+                         None, torch.bfloat16)
+    want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, np.float32([0.03125]), None, "bf16")
+    assert np.array_equal(storage(out, "bf16"), want)
+
+
+# ---------------------------------------------------------------- fused quant + GEMM
+
+
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+@pytest.mark.parametrize("shape", [(300, 520, 1024), (11712, 3072, 3072), (64, 12288, 3072)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_fused_quant_gemm_equals_unfused(xdt, shape):
+    m, n, k = shape
+    x = make_x(m, k, xdt, seed=11, dist="student_t").to(DEV)
+    w = make_w(n, k, seed=12).to(DEV)
+    ws = (torch.rand(n, generator=torch.Generator().manual_seed(13)) * 9e-3 + 1e-3).to(DEV)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(14)) * 0.02).to(torch.bfloat16).to(DEV)
+    q, xs = W.quantize_rowwise(x)
+    ref = W.gemm_dequant(q, w, xs, ws, bias, torch.bfloat16)
+    xs2 = W.row_scales(x)
+    fused = W.gemm_dequant_xq(x, xs2, w, ws, bias, torch.bfloat16)
+    assert torch.equal(xs, xs2)
+    assert torch.equal(ref.view(torch.int16), fused.view(torch.int16))
+
+
+def test_dequantize_linear_bit_exact():
+    m, n = 33, 70
+    g = torch.Generator().manual_seed(1)
+    acc = torch.randint(-2**24, 2**24, (m, n), generator=g, dtype=torch.int32)
+    xs = torch.rand(m, generator=g) * 0.1
+    ws = torch.rand(n, generator=g) * 0.01
+    bias = (torch.randn(n, generator=g) * 0.02).to(torch.float16)
+    out = W.dequantize_linear(acc.to(DEV), xs.to(DEV), ws.to(DEV), bias.to(DEV), torch.float16)
+    want = O.epilogue_kitchen(acc.numpy(), xs.numpy(), ws.numpy(), storage(bias, "f16"), "f16")
+    assert np.array_equal(storage(out, "f16"), want)
+
+
+# ---------------------------------------------------------------- operator vs reference payloads
+
+
+def _run_fixture(c, ops, scale_form, fused):
+    xd, od = OP.dtype_name(c["dtype"]), OP.dtype_name(c["output_dtype"])
+    x = from_storage(O.to_dtype(ops["x"], xd), xd)
+    w = torch.from_numpy(ops["weight"]).to(DEV)
+    ws = torch.from_numpy(np.asarray(ops["scale"])).to(DEV)
+    bias = None if ops["bias"] is None else torch.from_numpy(np.asarray(ops["bias"])).to(DEV)
+    out = W.int8_linear(x, w, ws, bias, TD[od], input_act=c.get("activation"),
+                        scale_form=scale_form, fused_quant=fused)
+    assert list(out.shape) == c["output_shape"]
+    return storage(out, od).reshape(-1), FX.payload(c, od)
+
+
+@pytest.mark.parametrize("section", sorted(FX.SECTIONS))
+@pytest.mark.parametrize("scale_form", ["ieee", "recip"])
+def test_operator_reproduces_reference_cuda_payloads(section, scale_form):
+    n = 0
+    for c, ops in FX.linear_cases(section):
+        got, want = _run_fixture(c, ops, scale_form, fused=False)
+        assert np.array_equal(got, want), c
+        n += 1
+    assert n > 100
+
+
+def test_operator_fused_quant_reproduces_gemm_payloads():
+    n = 0
+    for c, ops in FX.linear_cases("cuda_int8_gemm"):
+        got, want = _run_fixture(c, ops, "ieee", fused=True)
+        assert np.array_equal(got, want), c
+        n += 1
+    assert n > 100
+
+
+def test_operator_error_cases_match_reference_classes():
+    n = 0
+    for section in ("cuda_int8_gemm", "cuda_int8_gemv", "cuda_int8_m1"):
+        for c, ops in FX.linear_cases(section, with_errors=True):
+            xd, od = OP.dtype_name(c["dtype"]), OP.dtype_name(c["output_dtype"])
+            x = from_storage(O.to_dtype(ops["x"], xd), xd)
+            w = torch.from_numpy(ops["weight"]).to(DEV)
+            ws = torch.from_numpy(np.asarray(ops["scale"])).to(DEV)
+            r = None if ops["residual"] is None else torch.from_numpy(ops["residual"]).to(DEV)
+            rs = None if ops["residual_scale"] is None else torch.from_numpy(ops["residual_scale"]).to(DEV)
+            exc = {"ValueError": ValueError, "RuntimeError": RuntimeError}[c["error"]]
+            with pytest.raises(exc) as info:
+                W.int8_linear(x, w, ws, None, TD[od], residual=r, residual_scale=rs)
+            # Messages are compared for the reference's default policy (CUTLASS
+            # enabled); with COMFY_KITCHEN_DISABLE_CUTLASS the reference reports a
+            # bad GEMM scale from its cuBLAS dequant instead (same class).
+            if not c.get("disable_cutlass"):
+                assert str(info.value)[:48] == c["message"][:48], (c, str(info.value))
+            n += 1
+    assert n > 100
