@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/w8a8.h"
 
 namespace w8a8 {
@@ -37,8 +39,12 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 }
 
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
-    // The hardware conversion (v_cvt_f16_f32) rounds to nearest even in the
-    // default mode, including subnormal results and overflow to infinity.
+    // The empty asm pins f as an fp32 register value: without it the compiler
+    // may fuse the fp32 multiply-add that produced f and this conversion into
+    // one mixed-precision v_fma_mixlo_f16, which does not round like the two
+    // separate roundings (fp32, then fp16) this library computes.  The
+    // conversion itself (v_cvt_f16_f32) rounds to nearest even.
+    asm("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 
@@ -73,15 +79,41 @@ template <> struct DType<W8A8_BF16> {
 
 // ---------------------------------------------------------------- GELU (tanh)
 
-// 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3))), ATen's operation
-// order for the tanh approximation; the reference applies it as input_act
-// "gelu_tanh" (inference/src/int8_linear.rs:37-41).
+// gelu_tanh(x) = 0.5 * x * (1 + tanh(u)),  u = sqrt(2/pi) * (x + 0.044715 * x^3),
+// the reference's input_act "gelu_tanh" (inference/src/int8_linear.rs:37-41),
+// in ATen's operation order.  1 + tanh(u) is formed in fp32 exactly as the
+// reference forms it, so the cancellation of its negative tail matches.  Only
+// tanh itself is evaluated differently, from t = exp(-2|u|) (hardware exp2 and
+// reciprocal, about 1 ulp each): tanh(|u|) = 1 - 2t / (1 + t) for |u| >= 0.55,
+// where the error falls on the small term and the result is the correctly
+// rounded tanh up to rounding ties, and (1 - t) / (1 + t) below (absolute
+// error about 2^-24).
+__device__ __forceinline__ float tanh_fast(float u) {
+    const float kMinus2Log2e = -2.88539008177792681472f;  // -2 / ln(2)
+    const float a = fabsf(u);
+    const float t = __builtin_amdgcn_exp2f(a * kMinus2Log2e);  // (0, 1]
+    const float rc = __builtin_amdgcn_rcpf(1.0f + t);
+    const float r = a >= 0.55f ? 1.0f - (2.0f * t) * rc : (1.0f - t) * rc;
+    return __builtin_copysignf(r, u);
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
     const float kBeta = 0.79788456080286535588f;  // sqrt(2) * (2/sqrt(pi)) * 0.5
     const float kKappa = 0.044715f;
     float x_cube = x * x * x;
     float inner = kBeta * (x + kKappa * x_cube);
-    return 0.5f * x * (1.0f + tanhf(inner));
+    return 0.5f * x * (1.0f + tanh_fast(inner));
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
+// where an index selects a register array element (MFMA accumulators), so the
+// array can never be indexed dynamically (which would demote it to scratch).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
 }
 
 // ---------------------------------------------------------------- quantizer math

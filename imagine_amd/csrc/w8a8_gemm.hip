@@ -22,6 +22,9 @@
 // With XQ the activation tile is loaded as bf16/fp16 and quantized while it is
 // written to LDS (row constants from the row scales computed beforehand);
 // the codes are bit-identical to the standalone quantizer's.
+#include <cstdlib>
+#include <cstring>
+
 #include "w8a8_common.h"
 
 namespace w8a8 {
@@ -48,6 +51,84 @@ __device__ __forceinline__ TileCoord tile_of_block(int bid, int tiles_m, int til
     t.tm = first_m + in_group % gm;
     t.tn = in_group / gm;
     return t;
+}
+
+// Epilogue shared by both main loops.  For MFMA tile (i, j) a lane holds token
+// m = m_base + wave_m + 32 j + lane % 32 and channels
+// n = n_base + wave_n + 32 i + 8 g + 4 (lane / 32) + {0,1,2,3} in acc[i][j][4g .. 4g+3].
+// All accumulator indices are compile-time constants (static_for).
+template <int ODT, int MODE, bool GELU, int TN, int TM>
+__device__ __forceinline__ void store_tiles(const v16i (&acc)[TN][TM], int lane, int m_base,
+                                            int n_base, int wave_m, int wave_n, int M, int N,
+                                            const float* __restrict__ xs,
+                                            const float* __restrict__ ws, int64_t ws_size,
+                                            const void* __restrict__ bias, void* __restrict__ out) {
+    const int lane_m = lane % 32;
+    const int lane_n = 4 * (lane / 32);
+    float xsv[TM];
+    if constexpr (MODE == 0) {
+        static_for<0, TM>([&](auto j) {
+            const int m = m_base + wave_m + j * 32 + lane_m;
+            xsv[j] = xs[m < M ? m : M - 1];
+        });
+    }
+    const bool vec_ok = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+    static_for<0, TN>([&](auto i) {
+        static_for<0, 4>([&](auto g) {
+            const int n0 = n_base + wave_n + i * 32 + 8 * g + lane_n;
+            float wsv[4], bv[4];
+            if constexpr (MODE == 0) {
+                static_for<0, 4>([&](auto e) {
+                    const int n = n0 + e < N ? n0 + e : N - 1;
+                    wsv[e] = ws[ws_size == 1 ? 0 : n];
+                    bv[e] = bias ? DType<ODT>::load(
+                                       static_cast<const typename DType<ODT>::storage*>(bias)[n])
+                                 : 0.0f;
+                });
+            }
+            static_for<0, TM>([&](auto j) {
+                const int m = m_base + wave_m + j * 32 + lane_m;
+                if (m < M) {
+                    const int64_t row = static_cast<int64_t>(m) * N;
+                    if constexpr (MODE == 1) {
+                        int32_t* o = static_cast<int32_t*>(out) + row;
+                        if (vec_ok && n0 + 3 < N) {
+                            *reinterpret_cast<v4i*>(o + n0) =
+                                v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                    acc[i][j][4 * g + 3]};
+                        } else {
+                            static_for<0, 4>([&](auto e) {
+                                if (n0 + e < N) o[n0 + e] = acc[i][j][4 * g + e];
+                            });
+                        }
+                    } else {
+                        float v[4];
+                        static_for<0, 4>([&](auto e) {
+                            v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
+                        });
+                        using OS = typename DType<ODT>::storage;
+                        OS* o = static_cast<OS*>(out) + row;
+                        if (vec_ok && n0 + 3 < N) {
+                            if constexpr (ODT == W8A8_F32) {
+                                *reinterpret_cast<float4*>(o + n0) = make_float4(v[0], v[1], v[2], v[3]);
+                            } else {
+                                uint2 p;
+                                p.x = static_cast<uint32_t>(DType<ODT>::store(v[0])) |
+                                      (static_cast<uint32_t>(DType<ODT>::store(v[1])) << 16);
+                                p.y = static_cast<uint32_t>(DType<ODT>::store(v[2])) |
+                                      (static_cast<uint32_t>(DType<ODT>::store(v[3])) << 16);
+                                *reinterpret_cast<uint2*>(o + n0) = p;
+                            }
+                        } else {
+                            static_for<0, 4>([&](auto e) {
+                                if (n0 + e < N) o[n0 + e] = DType<ODT>::store(v[e]);
+                            });
+                        }
+                    }
+                }
+            });
+        });
+    });
 }
 
 template <int BN, int BM, int BK, int WN, int WM>
@@ -207,77 +288,182 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma(
         __syncthreads();
     }
 
-    // ---- epilogue: lane holds, for tile (i, j), token m = .. + lane % 32 and
-    // channels n = .. + 8 * g + 4 * (lane / 32) + {0,1,2,3} in acc[i][j][4g..4g+3].
-    const int lane_m = lane % 32;
-    const int lane_n = 4 * (lane / 32);
-    float xsv[S::TM];
-    if constexpr (MODE == 0) {
+    store_tiles<ODT, MODE, GELU, S::TN, S::TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
+                                               ws_size, bias, out);
+}
+
+// ---------------------------------------------------------------- LDS-DMA main loop
+//
+// Same tiling and epilogue as gemm_mfma, but the K tiles travel from global
+// memory straight into LDS (global_load_lds_dwordx4: each lane moves 16 bytes,
+// a wave fills 1 KB of contiguous LDS), through a ring of STAGES buffers, so
+// no VGPRs stage the tiles and no LDS write instructions are issued.  The LDS
+// tile is unpadded (BK bytes per row).  Bank conflicts of the 128-bit fragment
+// reads are avoided by an XOR swizzle of the 16-byte chunk index that depends
+// only on row mod 32 (so it is a per-lane constant):
+//   BK =  64 (4 chunks/row): chunk' = chunk ^ (((row >> 1) ^ (row >> 3)) & 3)
+//   BK = 128 (8 chunks/row): chunk' = chunk ^ ((row & 7) ^ ((row >> 3) & 3))
+// Either makes the rows read in one LDS cycle (8 consecutive rows for a
+// 128-byte-wide LDS, 16 for a 256-byte-wide one) land in distinct banks.  The
+// swizzle is applied on the load side by choosing which global chunk each
+// lane fetches.
+//
+// Synchronisation: one raw s_barrier per K tile, preceded by
+// s_waitcnt vmcnt(loads of later tiles) lgkmcnt(0): the wave's own DMA for
+// the tile about to be read has landed and its reads of the tile just
+// consumed have completed, so after the barrier every wave may read the new
+// tile and the buffer of the consumed one may be refilled.  The barrier is
+// crossed before the last k32 substep of a tile, so the LDS latency of the
+// next tile's first fragments hides under that substep's MFMAs.
+template <int BK>
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (BK == 64) return ((row >> 1) ^ (row >> 3)) & 3;
+    else return (row & 7) ^ ((row >> 3) & 3);
+}
+
+// s_waitcnt immediate for gfx9: vmcnt = n (0..63), expcnt unconstrained, lgkmcnt = 0.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | (((N >> 4) & 3) << 14));
+}
+
+#define W8A8_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+#define W8A8_GLB_PTR(p) ((const __attribute__((address_space(1))) void*)(p))
+
+template <int ODT, int MODE, bool GELU, int BK, int STAGES>
+__global__ __launch_bounds__(256, 1) void gemm_mfma_dma(
+    const int8_t* __restrict__ q, const int8_t* __restrict__ w, const float* __restrict__ xs,
+    const float* __restrict__ ws, int64_t ws_size, const void* __restrict__ bias,
+    void* __restrict__ out, int M, int N, int K, int group_m) {
+    constexpr int BN = 256, BM = 256, WN = 128, WM = 128;
+    constexpr int TN = WN / 32, TM = WM / 32;
+    constexpr int CPR = BK / 16;                           // 16-byte chunks per LDS row
+    constexpr int KS = BK / 32;                            // k32 substeps per tile
+    constexpr int kTileBytes = (BN + BM) * BK;             // one stage: weights then activations
+    constexpr int kWaveLoads = kTileBytes / 1024;          // 1 KB per wave-load
+    constexpr int kLoadsPerThread = kWaveLoads / 4;        // 4 waves
+    constexpr int kWWaveLoads = BN * BK / 1024;
+    static_assert(kLoadsPerThread * (STAGES - 2) < 64, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[STAGES * kTileBytes];
+
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n, group_m);
+    const int m_base = tc.tm * BM, n_base = tc.tn * BN;
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    const int wave_n = (wave % (BN / WN)) * WN;
+    const int wave_m = (wave / (BN / WN)) * WM;
+    const int KT = K / BK;                                 // K % BK == 0 (host checks)
+
+    // Source of each wave-load this lane takes part in: wave-load L (global
+    // index wave * kLoadsPerThread + j) fills LDS chunks [64 L, 64 L + 64) of the
+    // stage; chunk p holds row p / CPR, logical chunk (p % CPR) ^ swz(row).
+    uint32_t src_off[kLoadsPerThread];
 #pragma unroll
-        for (int j = 0; j < S::TM; ++j) {
-            const int m = m_base + wave_m + j * 32 + lane_m;
-            xsv[j] = xs[m < M ? m : M - 1];
-        }
+    for (int j = 0; j < kLoadsPerThread; ++j) {
+        const int L = wave * kLoadsPerThread + j;
+        const bool is_w = L < kWWaveLoads;
+        const int p = (is_w ? L : L - kWWaveLoads) * 64 + lane;
+        const int r = p / CPR;
+        const int c = (p % CPR) ^ swz<BK>(r);
+        int row = (is_w ? n_base : m_base) + r;
+        const int lim = is_w ? N : M;
+        row = row < lim ? row : lim - 1;
+        src_off[j] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + c * 16;
     }
-    const bool vec_ok = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+    auto issue = [&](int kt, int stage) {
+        const uint32_t k0 = static_cast<uint32_t>(kt) * BK;
 #pragma unroll
-    for (int i = 0; i < S::TN; ++i) {
+        for (int j = 0; j < kLoadsPerThread; ++j) {
+            const int L = wave * kLoadsPerThread + j;
+            const int8_t* src = (L < kWWaveLoads ? w : q) + src_off[j] + k0;
+            __builtin_amdgcn_global_load_lds(W8A8_GLB_PTR(src),
+                                             W8A8_LDS_PTR(lds + stage * kTileBytes + L * 1024), 16, 0, 0);
+        }
+    };
+
+    v16i acc[TN][TM];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int n0 = n_base + wave_n + i * 32 + 8 * g + lane_n;
-            float wsv[4], bv[4];
-            if constexpr (MODE == 0) {
+    for (int i = 0; i < TN; ++i)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int n = n0 + e < N ? n0 + e : N - 1;
-                    wsv[e] = ws[ws_size == 1 ? 0 : n];
-                    bv[e] = bias ? DType<ODT>::load(
-                                       static_cast<const typename DType<ODT>::storage*>(bias)[n])
-                                 : 0.0f;
+        for (int j = 0; j < TM; ++j) acc[i][j] = v16i{};
+
+    const int fl = swz<BK>(lane % 32);
+    int rd[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) rd[ks] = (((2 * ks + lane / 32) ^ fl) * 16);
+    const int wrow = (wave_n + lane % 32) * BK;
+    const int xrow = (BN + wave_m + lane % 32) * BK;
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < KT) issue(s, s);
+
+    // Fragments of one k32 substep: TN weight fragments, TM activation fragments.
+    auto read_frags = [&](int stage, int ks, v4i (&a)[TN], v4i (&b)[TM]) {
+        const int8_t* base = lds + stage * kTileBytes + rd[ks];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+            a[i] = *reinterpret_cast<const v4i*>(base + wrow + i * 32 * BK);
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+            b[j] = *reinterpret_cast<const v4i*>(base + xrow + j * 32 * BK);
+    };
+    auto mfmas = [&](const v4i (&a)[TN], const v4i (&b)[TM]) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+    };
+    // Wait until this wave's DMA for the next tile has landed (at most `after`
+    // later tiles still in flight) and its LDS reads have completed.
+    auto wait_tile = [&](int after) {
+        if constexpr (STAGES >= 4) {
+            if (after >= 2) { wait_vm_lgkm0<2 * kLoadsPerThread>(); return; }
+        }
+        if constexpr (STAGES >= 3) {
+            if (after >= 1) { wait_vm_lgkm0<kLoadsPerThread>(); return; }
+        }
+        wait_vm_lgkm0<0>();
+    };
+
+    v4i fa[2][TN], fb[2][TM];   // two fragment sets, alternating by substep parity
+    if (KT > 0) {
+        wait_tile(KT - 1 < STAGES - 2 ? KT - 1 : STAGES - 2);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        if (STAGES - 1 < KT) issue(STAGES - 1, STAGES - 1);
+        read_frags(0, 0, fa[0], fb[0]);
+    }
+    int stage = 0;
+    for (int kt = 0; kt < KT; ++kt) {
+        const bool more = kt + 1 < KT;
+        const int next = stage + 1 == STAGES ? 0 : stage + 1;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int cur = ks & 1;
+            if (ks + 1 < KS) {
+                read_frags(stage, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                mfmas(fa[cur], fb[cur]);
+            } else {
+                if (more) {
+                    // tiles issued so far: up to min(KT - 1, kt + STAGES - 1)
+                    const int last = KT - 1 < kt + STAGES - 1 ? KT - 1 : kt + STAGES - 1;
+                    wait_tile(last - (kt + 1));
+                    __builtin_amdgcn_s_barrier();
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (kt + STAGES < KT) issue(kt + STAGES, stage);
+                    read_frags(next, 0, fa[cur ^ 1], fb[cur ^ 1]);
                 }
-            }
-#pragma unroll
-            for (int j = 0; j < S::TM; ++j) {
-                const int m = m_base + wave_m + j * 32 + lane_m;
-                if (m >= M) continue;
-                const int64_t row = static_cast<int64_t>(m) * N;
-                if constexpr (MODE == 1) {
-                    int32_t* o = static_cast<int32_t*>(out) + row;
-                    if (vec_ok && n0 + 3 < N) {
-                        *reinterpret_cast<v4i*>(o + n0) =
-                            v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (n0 + e < N) o[n0 + e] = acc[i][j][4 * g + e];
-                    }
-                } else {
-                    float v[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
-                    using OS = typename DType<ODT>::storage;
-                    OS* o = static_cast<OS*>(out) + row;
-                    if (vec_ok && n0 + 3 < N) {
-                        if constexpr (ODT == W8A8_F32) {
-                            *reinterpret_cast<float4*>(o + n0) = make_float4(v[0], v[1], v[2], v[3]);
-                        } else {
-                            uint2 p;
-                            p.x = static_cast<uint32_t>(DType<ODT>::store(v[0])) |
-                                  (static_cast<uint32_t>(DType<ODT>::store(v[1])) << 16);
-                            p.y = static_cast<uint32_t>(DType<ODT>::store(v[2])) |
-                                  (static_cast<uint32_t>(DType<ODT>::store(v[3])) << 16);
-                            *reinterpret_cast<uint2*>(o + n0) = p;
-                        }
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (n0 + e < N) o[n0 + e] = DType<ODT>::store(v[e]);
-                    }
-                }
+                mfmas(fa[cur], fb[cur]);
             }
         }
+        stage = next;
     }
+
+    store_tiles<ODT, MODE, GELU, TN, TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
+                                         ws_size, bias, out);
 }
 
 // Generic GEMM for shapes the MFMA kernel does not take (K % 16 != 0,
@@ -342,17 +528,62 @@ bool gemm_mfma_supported(const void* a, size_t a_elem, const int8_t* w, int64_t 
            M * K * static_cast<int64_t>(a_elem) < (1ll << 40);
 }
 
+// Main-loop choice for the int8-input GEMM: the LDS-DMA ring (default
+// BK = 128, 2 stages) or the register-staged double buffer.
+// W8A8_GEMM_MAINLOOP = regs | dma64x3 | dma64x4 | dma128x2 selects one (a
+// tuning knob; every choice produces identical results).
+static int mainloop_choice() {
+    static int choice = [] {
+        const char* e = std::getenv("W8A8_GEMM_MAINLOOP");
+        if (!e) return 3;
+        if (std::strcmp(e, "regs") == 0) return 0;
+        if (std::strcmp(e, "dma64x3") == 0) return 1;
+        if (std::strcmp(e, "dma64x4") == 0) return 2;
+        return 3;
+    }();
+    return choice;
+}
+
+template <int ODT, int MODE, bool GELU, int BK, int STAGES>
+static void launch_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                       int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
+                       hipStream_t stream) {
+    const int tiles = static_cast<int>(((M + 255) / 256) * ((N + 255) / 256));
+    hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, BK, STAGES>), dim3(tiles), dim3(256), 0, stream,
+                       q, w, xs, ws, ws_size, bias, out, static_cast<int>(M), static_cast<int>(N),
+                       static_cast<int>(K), kGroupM);
+}
+
+template <int ODT, int MODE, bool GELU>
+static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                    int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
+                    hipStream_t stream) {
+    const int choice = mainloop_choice();
+    // 32-bit source offsets; whole K tiles only (the DMA ring has no tail masking)
+    if (choice == 0 || M * K >= (1ll << 32) - 4096 || N * K >= (1ll << 32) - 4096) return false;
+    if (choice == 3 && K % 128 == 0) {
+        launch_dma<ODT, MODE, GELU, 128, 2>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+        return true;
+    }
+    if (K % 64 != 0) return false;
+    if (choice == 2) launch_dma<ODT, MODE, GELU, 64, 4>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+    else launch_dma<ODT, MODE, GELU, 64, 3>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+    return true;
+}
+
 template <int ODT, bool GELU>
 static void gemm_dispatch_odt(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                               int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N,
                               int64_t K, bool int32_out, hipStream_t stream) {
     const bool fast = gemm_mfma_supported(q, 1, w, M, N, K);
     if (int32_out) {
+        if (fast && try_dma<ODT, 1, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream)) return;
         if (fast) launch_mfma<ODT, 1, false, -1>(q, nullptr, w, xs, ws, ws_size, bias, out, M, N, K, stream);
         else hipLaunchKernelGGL((gemm_generic<ODT, 1, false>), dim3(static_cast<unsigned>((M * N + 255) / 256)),
                                 dim3(256), 0, stream, q, w, xs, ws, ws_size, bias, out, M, N, K);
         return;
     }
+    if (fast && try_dma<ODT, 0, GELU>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream)) return;
     if (fast) launch_mfma<ODT, 0, GELU, -1>(q, nullptr, w, xs, ws, ws_size, bias, out, M, N, K, stream);
     else hipLaunchKernelGGL((gemm_generic<ODT, 0, GELU>), dim3(static_cast<unsigned>((M * N + 255) / 256)),
                             dim3(256), 0, stream, q, w, xs, ws, ws_size, bias, out, M, N, K);

@@ -180,8 +180,11 @@ def test_gemm_dequant_epilogue_bit_exact(odt, with_bias, ws_scalar):
     assert np.array_equal(storage(out, odt), want)
 
 
-@pytest.mark.parametrize("odt", ["bf16", "f16"])
+@pytest.mark.parametrize("odt", ["bf16", "f16", "f32"])
 def test_gemm_gelu_epilogue_within_one_ulp(odt):
+    """GELU-tanh epilogue: within one output ulp of the oracle (libm tanhf form)
+    plus an absolute 2^-22 for the saturated negative tail; fp32 outputs, which
+    no 16-bit rounding hides, within 2^-18 relative."""
     m, n, k = 260, 384, 768
     x = make_x(m, k, "bf16", seed=8)
     q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
@@ -193,8 +196,15 @@ def test_gemm_gelu_epilogue_within_one_ulp(odt):
     want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt),
                               odt, act=1)
     got = storage(out, odt)
-    assert ulp_close(got, want, odt, abs_floor=2.0**-22).all()
-    assert (got == want).mean() > 0.999
+    a = O.to_f32(got, odt).astype(np.float64)
+    b = O.to_f32(want, odt).astype(np.float64)
+    rel = {"bf16": 2.0**-7, "f16": 2.0**-10, "f32": 2.0**-18}[odt]
+    bad = np.abs(a - b) > np.abs(b) * rel + 2.0**-22
+    if bad.any():
+        i = np.argmax(np.abs(a - b) - np.abs(b) * rel)
+        pytest.fail(f"{int(bad.sum())} outputs off; worst got {a.flat[i]!r} want {b.flat[i]!r}")
+    if odt != "f32":
+        assert (got == want).mean() > 0.999
 
 
 def test_gemm_full_size_sampled_rows_bit_exact():
