@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--only", default=None,
                    help="run only one kernel in a loop (for rocprofv3 counters): "
-                        "up_gemm | quant | gemv | xq_gemm")
+                        "up_gemm | quant | step | copy")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     return p.parse_args()
@@ -329,6 +329,13 @@ def run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs):
     elif args.only == "step":
         for _ in range(n_iter):
             step()
+    elif args.only == "copy":
+        # counter calibration: a plain device copy of known size (1 GiB read,
+        # 1 GiB written per launch) for scaling FETCH_SIZE / WRITE_SIZE
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(n_iter):
+            dst.copy_(src)
     else:
         raise SystemExit(f"unknown --only {args.only}")
     torch.cuda.synchronize()
