@@ -294,13 +294,13 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma(
 
 // ---------------------------------------------------------------- LDS-DMA main loop
 //
-// Same tiling and epilogue as gemm_mfma, but the K tiles travel from global
-// memory straight into LDS (global_load_lds_dwordx4: each lane moves 16 bytes,
-// a wave fills 1 KB of contiguous LDS), through a ring of STAGES buffers, so
-// no VGPRs stage the tiles and no LDS write instructions are issued.  The LDS
-// tile is unpadded (BK bytes per row).  Bank conflicts of the 128-bit fragment
-// reads are avoided by an XOR swizzle of the 16-byte chunk index that depends
-// only on row mod 32 (so it is a per-lane constant):
+// Same MFMA tiling and accumulator layout as gemm_mfma, but the K tiles travel
+// from global memory straight into LDS (global_load_lds_dwordx4: each lane
+// moves 16 bytes, a wave fills 1 KB of contiguous LDS), through a ring of
+// STAGES buffers, so no VGPRs stage the tiles and no LDS write instructions
+// are issued.  The LDS tile is unpadded (BK bytes per row).  Bank conflicts of
+// the 128-bit fragment reads are avoided by an XOR swizzle of the 16-byte
+// chunk index that depends only on row mod 32 (so it is a per-lane constant):
 //   BK =  64 (4 chunks/row): chunk' = chunk ^ (((row >> 1) ^ (row >> 3)) & 3)
 //   BK = 128 (8 chunks/row): chunk' = chunk ^ ((row & 7) ^ ((row >> 3) & 3))
 // Either makes the rows read in one LDS cycle (8 consecutive rows for a
@@ -308,13 +308,24 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma(
 // swizzle is applied on the load side by choosing which global chunk each
 // lane fetches.
 //
+// Occupancy: OCC blocks of 4 waves per CU (OCC = 2 keeps each wave within 256
+// registers, 128 of them accumulators), so one block's epilogue and barrier
+// waits run under the other block's MFMAs.
+//
 // Synchronisation: one raw s_barrier per K tile, preceded by
 // s_waitcnt vmcnt(loads of later tiles) lgkmcnt(0): the wave's own DMA for
 // the tile about to be read has landed and its reads of the tile just
 // consumed have completed, so after the barrier every wave may read the new
 // tile and the buffer of the consumed one may be refilled.  The barrier is
 // crossed before the last k32 substep of a tile, so the LDS latency of the
-// next tile's first fragments hides under that substep's MFMAs.
+// next tile's first fragments hides under that substep's MFMAs.  Inside a
+// substep the fragment reads of the next substep are interleaved one by one
+// with the MFMAs (sched_group_barrier), which keeps two fragment sets live.
+//
+// Epilogue of 16-bit outputs: the block's dequantized tile is staged through
+// the (then idle) LDS ring, rows of BN values with the 16-byte chunk index
+// XOR-swizzled by the row, and leaves as full-row 16-byte-per-lane stores, so
+// every output line is written whole.
 template <int BK>
 __device__ __forceinline__ int swz(int row) {
     if constexpr (BK == 64) return ((row >> 1) ^ (row >> 3)) & 3;
@@ -331,21 +342,106 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 #define W8A8_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
 #define W8A8_GLB_PTR(p) ((const __attribute__((address_space(1))) void*)(p))
 
-template <int ODT, int MODE, bool GELU, int BK, int STAGES>
-__global__ __launch_bounds__(256, 1) void gemm_mfma_dma(
+// sched_group_barrier masks
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedVmem = 0x010;
+constexpr int kSchedDsRead = 0x100;
+
+template <int BN_, int BM_, int WN_, int WM_, int BK_, int STAGES_, int OCC_>
+struct DmaCfg {
+    static constexpr int BN = BN_, BM = BM_, WN = WN_, WM = WM_, BK = BK_, STAGES = STAGES_, OCC = OCC_;
+    static_assert((BN / WN) * (BM / WM) == 4, "4 waves per block");
+    static constexpr int TN = WN / 32, TM = WM / 32;       // MFMA tiles per wave
+    static constexpr int CPR = BK / 16;                    // 16-byte chunks per LDS row
+    static constexpr int KS = BK / 32;                     // k32 substeps per tile
+    static constexpr int kTileBytes = (BN + BM) * BK;      // one stage: weights then activations
+    static constexpr int kWaveLoads = kTileBytes / 1024;   // 1 KB per wave-load
+    static_assert(kWaveLoads % 4 == 0, "wave-loads split evenly over 4 waves");
+    static constexpr int kLoadsPerThread = kWaveLoads / 4;
+    static constexpr int kWWaveLoads = BN * BK / 1024;
+    static_assert(kLoadsPerThread * (STAGES - 2) < 64, "vmcnt range");
+    static constexpr int kLds = STAGES * kTileBytes;
+    // 16-bit output tile staged through LDS for whole-line stores
+    static constexpr bool kStageOut = BN * BM * 2 <= kLds;
+};
+
+// The 16-byte output chunk c of staged row r sits at chunk c ^ (r mod chunks-per-row, up to 32).
+template <int BN>
+__device__ __forceinline__ int out_swz(int row) {
+    constexpr int kChunks = BN / 8;
+    return row & ((kChunks < 32 ? kChunks : 32) - 1);
+}
+
+// Dequantize the block's accumulators into the LDS ring as a BM x BN tile of
+// 16-bit values, then write it out row by row, 16 bytes per lane (N % 8 == 0,
+// 16-byte aligned out).  Same values as store_tiles.
+template <int ODT, bool GELU, class C>
+__device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::TM], int8_t* lds,
+                                                   int lane, int t, int m_base, int n_base,
+                                                   int wave_m, int wave_n, int M, int N,
+                                                   const float* __restrict__ xs,
+                                                   const float* __restrict__ ws, int64_t ws_size,
+                                                   const void* __restrict__ bias,
+                                                   void* __restrict__ out) {
+    constexpr int BN = C::BN, BM = C::BM, TN = C::TN, TM = C::TM;
+    constexpr int kRowBytes = BN * 2;
+    constexpr int kChunks = BN / 8;   // 16-byte chunks per staged row
+    using OS = typename DType<ODT>::storage;
+    const int lane_m = lane % 32, half = lane / 32;
+    float xsv[TM];
+    static_for<0, TM>([&](auto j) {
+        const int m = m_base + wave_m + j * 32 + lane_m;
+        xsv[j] = xs[m < M ? m : M - 1];
+    });
+    __syncthreads();  // every wave has finished reading the last K tile
+    static_for<0, TN>([&](auto i) {
+        static_for<0, 4>([&](auto g) {
+            const int chunk = (wave_n + i * 32 + 8 * g) / 8;
+            const int n0 = n_base + wave_n + i * 32 + 8 * g + 4 * half;
+            float wsv[4], bv[4];
+            static_for<0, 4>([&](auto e) {
+                const int n = n0 + e < N ? n0 + e : N - 1;
+                wsv[e] = ws[ws_size == 1 ? 0 : n];
+                bv[e] = bias ? DType<ODT>::load(static_cast<const OS*>(bias)[n]) : 0.0f;
+            });
+            static_for<0, TM>([&](auto j) {
+                const int ml = wave_m + j * 32 + lane_m;
+                float v[4];
+                static_for<0, 4>([&](auto e) {
+                    v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
+                });
+                uint2 p;
+                p.x = static_cast<uint32_t>(DType<ODT>::store(v[0])) |
+                      (static_cast<uint32_t>(DType<ODT>::store(v[1])) << 16);
+                p.y = static_cast<uint32_t>(DType<ODT>::store(v[2])) |
+                      (static_cast<uint32_t>(DType<ODT>::store(v[3])) << 16);
+                *reinterpret_cast<uint2*>(lds + ml * kRowBytes + (chunk ^ out_swz<BN>(ml)) * 16 + half * 8) = p;
+            });
+        });
+    });
+    __syncthreads();
+    constexpr int kTotal = BM * kChunks;
+    static_assert(kTotal % 256 == 0, "whole passes of 256 chunks");
+#pragma unroll 4
+    for (int pass = 0; pass < kTotal / 256; ++pass) {
+        const int idx = pass * 256 + t;
+        const int r = idx / kChunks, c = idx % kChunks;
+        const int m = m_base + r, n = n_base + c * 8;
+        const uint4 v = *reinterpret_cast<const uint4*>(lds + r * kRowBytes + (c ^ out_swz<BN>(r)) * 16);
+        if (m < M && n < N) *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
+    }
+}
+
+template <int ODT, int MODE, bool GELU, class C>
+__global__ __launch_bounds__(256, C::OCC) void gemm_mfma_dma(
     const int8_t* __restrict__ q, const int8_t* __restrict__ w, const float* __restrict__ xs,
     const float* __restrict__ ws, int64_t ws_size, const void* __restrict__ bias,
     void* __restrict__ out, int M, int N, int K, int group_m) {
-    constexpr int BN = 256, BM = 256, WN = 128, WM = 128;
-    constexpr int TN = WN / 32, TM = WM / 32;
-    constexpr int CPR = BK / 16;                           // 16-byte chunks per LDS row
-    constexpr int KS = BK / 32;                            // k32 substeps per tile
-    constexpr int kTileBytes = (BN + BM) * BK;             // one stage: weights then activations
-    constexpr int kWaveLoads = kTileBytes / 1024;          // 1 KB per wave-load
-    constexpr int kLoadsPerThread = kWaveLoads / 4;        // 4 waves
-    constexpr int kWWaveLoads = BN * BK / 1024;
-    static_assert(kLoadsPerThread * (STAGES - 2) < 64, "vmcnt range");
-    __shared__ __attribute__((aligned(1024))) int8_t lds[STAGES * kTileBytes];
+    constexpr int BN = C::BN, BM = C::BM, WN = C::WN, WM = C::WM, BK = C::BK, STAGES = C::STAGES;
+    constexpr int TN = C::TN, TM = C::TM, CPR = C::CPR, KS = C::KS;
+    constexpr int kTileBytes = C::kTileBytes, kLoadsPerThread = C::kLoadsPerThread;
+    constexpr int kWWaveLoads = C::kWWaveLoads;
+    __shared__ __attribute__((aligned(1024))) int8_t lds[C::kLds];
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n, group_m);
@@ -358,7 +454,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_dma(
     // Source of each wave-load this lane takes part in: wave-load L (global
     // index wave * kLoadsPerThread + j) fills LDS chunks [64 L, 64 L + 64) of the
     // stage; chunk p holds row p / CPR, logical chunk (p % CPR) ^ swz(row).
-    uint32_t src_off[kLoadsPerThread];
+    const int8_t* src[kLoadsPerThread];
 #pragma unroll
     for (int j = 0; j < kLoadsPerThread; ++j) {
         const int L = wave * kLoadsPerThread + j;
@@ -369,15 +465,14 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_dma(
         int row = (is_w ? n_base : m_base) + r;
         const int lim = is_w ? N : M;
         row = row < lim ? row : lim - 1;
-        src_off[j] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + c * 16;
+        src[j] = (is_w ? w : q) + static_cast<int64_t>(row) * K + c * 16;
     }
     auto issue = [&](int kt, int stage) {
-        const uint32_t k0 = static_cast<uint32_t>(kt) * BK;
+        const int k0 = kt * BK;
 #pragma unroll
         for (int j = 0; j < kLoadsPerThread; ++j) {
             const int L = wave * kLoadsPerThread + j;
-            const int8_t* src = (L < kWWaveLoads ? w : q) + src_off[j] + k0;
-            __builtin_amdgcn_global_load_lds(W8A8_GLB_PTR(src),
+            __builtin_amdgcn_global_load_lds(W8A8_GLB_PTR(src[j] + k0),
                                              W8A8_LDS_PTR(lds + stage * kTileBytes + L * 1024), 16, 0, 0);
         }
     };
@@ -416,6 +511,18 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_dma(
             for (int j = 0; j < TM; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
     };
+    // One MFMA, then one fragment read, while reads remain; then the rest of
+    // the MFMAs.
+    auto interleave = [&]() {
+        constexpr int kReads = TN + TM, kMfma = TN * TM;
+        constexpr int kPairs = kReads < kMfma ? kReads : kMfma;
+        static_for<0, kPairs>([&](auto) {
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        });
+        if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(kSchedMfma, kMfma - kPairs, 0);
+        if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReads - kPairs, 0);
+    };
     // Wait until this wave's DMA for the next tile has landed (at most `after`
     // later tiles still in flight) and its LDS reads have completed.
     auto wait_tile = [&](int after) {
@@ -438,30 +545,42 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma_dma(
     }
     int stage = 0;
     for (int kt = 0; kt < KT; ++kt) {
-        const bool more = kt + 1 < KT;
         const int next = stage + 1 == STAGES ? 0 : stage + 1;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             const int cur = ks & 1;
             if (ks + 1 < KS) {
                 read_frags(stage, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
-                mfmas(fa[cur], fb[cur]);
             } else {
-                if (more) {
+                if (kt + 1 < KT) {
                     // tiles issued so far: up to min(KT - 1, kt + STAGES - 1)
                     const int last = KT - 1 < kt + STAGES - 1 ? KT - 1 : kt + STAGES - 1;
                     wait_tile(last - (kt + 1));
                     __builtin_amdgcn_s_barrier();
                     __builtin_amdgcn_sched_barrier(0);
                     if (kt + STAGES < KT) issue(kt + STAGES, stage);
-                    read_frags(next, 0, fa[cur ^ 1], fb[cur ^ 1]);
                 }
-                mfmas(fa[cur], fb[cur]);
+                // first fragments of the next tile (after the last tile: an
+                // unused in-bounds read, which keeps this one basic block)
+                read_frags(next, 0, fa[cur ^ 1], fb[cur ^ 1]);
             }
+            // The single MFMA block of the substep: one copy only, so the
+            // accumulators stay in AGPRs.
+            mfmas(fa[cur], fb[cur]);
+            interleave();
+            __builtin_amdgcn_sched_barrier(0);
         }
         stage = next;
     }
 
+    if constexpr (MODE == 0 && ODT != W8A8_F32 && C::kStageOut) {
+        const bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+        if (vec_ok) {
+            store_tiles_staged<ODT, GELU, C>(acc, lds, lane, t, m_base, n_base, wave_m, wave_n, M, N,
+                                             xs, ws, ws_size, bias, out);
+            return;
+        }
+    }
     store_tiles<ODT, MODE, GELU, TN, TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
                                          ws_size, bias, out);
 }
@@ -528,28 +647,32 @@ bool gemm_mfma_supported(const void* a, size_t a_elem, const int8_t* w, int64_t 
            M * K * static_cast<int64_t>(a_elem) < (1ll << 40);
 }
 
-// Main-loop choice for the int8-input GEMM: the LDS-DMA ring (default
-// BK = 128, 2 stages) or the register-staged double buffer.
-// W8A8_GEMM_MAINLOOP = regs | dma64x3 | dma64x4 | dma128x2 selects one (a
+// Main-loop configurations of the int8-input GEMM (weights BN x activations BM
+// per block, wave tile WN x WM, BK bytes per K tile, ring depth, blocks per CU).
+using CfgN256M128 = DmaCfg<256, 128, 128, 64, 64, 3, 2>;
+using CfgN128M256 = DmaCfg<128, 256, 64, 128, 64, 3, 2>;
+using CfgN256M256 = DmaCfg<256, 256, 128, 128, 128, 2, 1>;
+
+// W8A8_GEMM_MAINLOOP = n256m128 | n128m256 | n256m256 | regs selects one (a
 // tuning knob; every choice produces identical results).
 static int mainloop_choice() {
     static int choice = [] {
         const char* e = std::getenv("W8A8_GEMM_MAINLOOP");
-        if (!e) return 3;
+        if (!e) return 1;
         if (std::strcmp(e, "regs") == 0) return 0;
-        if (std::strcmp(e, "dma64x3") == 0) return 1;
-        if (std::strcmp(e, "dma64x4") == 0) return 2;
-        return 3;
+        if (std::strcmp(e, "n128m256") == 0) return 2;
+        if (std::strcmp(e, "n256m256") == 0) return 3;
+        return 1;
     }();
     return choice;
 }
 
-template <int ODT, int MODE, bool GELU, int BK, int STAGES>
+template <int ODT, int MODE, bool GELU, class C>
 static void launch_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                        int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
                        hipStream_t stream) {
-    const int tiles = static_cast<int>(((M + 255) / 256) * ((N + 255) / 256));
-    hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, BK, STAGES>), dim3(tiles), dim3(256), 0, stream,
+    const int tiles = static_cast<int>(((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN));
+    hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C>), dim3(tiles), dim3(256), 0, stream,
                        q, w, xs, ws, ws_size, bias, out, static_cast<int>(M), static_cast<int>(N),
                        static_cast<int>(K), kGroupM);
 }
@@ -559,15 +682,16 @@ static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const flo
                     int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
                     hipStream_t stream) {
     const int choice = mainloop_choice();
-    // 32-bit source offsets; whole K tiles only (the DMA ring has no tail masking)
-    if (choice == 0 || M * K >= (1ll << 32) - 4096 || N * K >= (1ll << 32) - 4096) return false;
-    if (choice == 3 && K % 128 == 0) {
-        launch_dma<ODT, MODE, GELU, 128, 2>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+    // whole K tiles only (the DMA ring has no tail masking)
+    if (choice == 0) return false;
+    if (choice == 3) {
+        if (K % CfgN256M256::BK != 0) return false;
+        launch_dma<ODT, MODE, GELU, CfgN256M256>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
         return true;
     }
     if (K % 64 != 0) return false;
-    if (choice == 2) launch_dma<ODT, MODE, GELU, 64, 4>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
-    else launch_dma<ODT, MODE, GELU, 64, 3>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+    if (choice == 2) launch_dma<ODT, MODE, GELU, CfgN128M256>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+    else launch_dma<ODT, MODE, GELU, CfgN256M128>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
     return true;
 }
 
