@@ -26,12 +26,21 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round to nearest even (finite inputs; NaN keeps a quiet payload).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round to nearest even, one v_cvt_pk_bf16_f32 (gfx950).  Bit-identical to
+// the software form u += 0x7fff + ((u >> 16) & 1) for every finite input,
+// denormals included, and NaN -> (u >> 16) | 0x40 (checked on all 2^32
+// inputs on the device).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return static_cast<uint16_t>(u >> 16);
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// Two values rounded as above and packed (a in the low half), one instruction.
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+    const f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
@@ -63,6 +72,9 @@ template <> struct DType<W8A8_F16> {
     static constexpr int bytes = 2;
     __device__ static float load(const storage v) { return f16_to_f32(v); }
     __device__ static storage store(float f) { return f32_to_f16(f); }
+    __device__ static uint32_t store2(float a, float b) {
+        return static_cast<uint32_t>(f32_to_f16(a)) | (static_cast<uint32_t>(f32_to_f16(b)) << 16);
+    }
     __device__ static float round(float f) { return f16_to_f32(f32_to_f16(f)); }
     static constexpr float finite_max = 65504.0f;
     static constexpr float tiny = 6.103515625e-5f;
@@ -72,6 +84,7 @@ template <> struct DType<W8A8_BF16> {
     static constexpr int bytes = 2;
     __device__ static float load(const storage v) { return bf16_to_f32(v); }
     __device__ static storage store(float f) { return f32_to_bf16(f); }
+    __device__ static uint32_t store2(float a, float b) { return pack2_bf16(a, b); }
     __device__ static float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
     static constexpr float finite_max = 3.38953139e38f;
     static constexpr float tiny = 1.17549435e-38f;

@@ -1,629 +1,11 @@
-// INT8 x INT8 -> INT32 GEMM with the fused dequant epilogue, for gfx950 MFMA.
-//
-// Replaces Kitchen's CUTLASS FusedInt8Gemm (cutlass_gemm_int8.cu:63-120, entry
-// launch_cutlass_int8_dequant :373-388) and, in the int32 mode, the cuBLASLt
-// int32 GEMM (cublas_gemm_int8.cu:176-221):
-//   out[m, n] = O( fma(float(sum_k q[m,k] * w[n,k]) * xs[m], ws[n], bias[n]) )
-//
-// Tiling (CDNA4, wave64):
-//   * block tile BN (weight rows n) x BM (activation rows m) x BK (k bytes),
-//     256 threads = 4 waves in a 2 x 2 grid, each wave WN x WM;
-//   * v_mfma_i32_32x32x32_i8: the weight tile is the MFMA A operand and the
-//     activation tile the B operand, so the accumulator registers of a lane
-//     hold 4 consecutive output channels n of one token m -> 8-byte bf16 stores;
-//   * K tiles staged through LDS, double buffered: global 128-bit loads of
-//     tile k+1 are in flight while tile k is multiplied; LDS rows are padded by
-//     16 bytes so the 128-bit fragment reads of 8/16 consecutive rows hit
-//     distinct banks;
-//   * tile order: blocks are remapped so that the blocks one XCD runs are
-//     contiguous in tile space (the hardware deals blocks to the 8 XCDs
-//     round-robin), then grouped GROUP_M activation tiles at a time, so each
-//     XCD's L2 sees a small window of weight and activation rows.
-// With XQ the activation tile is loaded as bf16/fp16 and quantized while it is
-// written to LDS (row constants from the row scales computed beforehand);
-// the codes are bit-identical to the standalone quantizer's.
+// Host-side dispatch of the W8A8 GEMM kernels (w8a8_gemm_kernels.h): choice
+// of main loop and tile configuration, launch, and the C-ABI-facing launchers.
 #include <cstdlib>
 #include <cstring>
 
-#include "w8a8_common.h"
+#include "w8a8_gemm_kernels.h"
 
 namespace w8a8 {
-
-constexpr int kXcds = 8;
-
-struct TileCoord {
-    int tm, tn;
-};
-
-// Bijective remap of the launch order so that consecutive blocks dealt to one
-// XCD take consecutive tiles, then a grouped (GROUP_M tall) walk of tile space.
-__device__ __forceinline__ TileCoord tile_of_block(int bid, int tiles_m, int tiles_n, int group_m) {
-    const int total = tiles_m * tiles_n;
-    const int per = total / kXcds, rem = total % kXcds;
-    const int xcd = bid % kXcds;
-    const int logical = xcd * per + (xcd < rem ? xcd : rem) + bid / kXcds;
-    const int group_size = group_m * tiles_n;
-    const int group = logical / group_size;
-    const int first_m = group * group_m;
-    const int gm = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
-    const int in_group = logical % group_size;
-    TileCoord t;
-    t.tm = first_m + in_group % gm;
-    t.tn = in_group / gm;
-    return t;
-}
-
-// Epilogue shared by both main loops.  For MFMA tile (i, j) a lane holds token
-// m = m_base + wave_m + 32 j + lane % 32 and channels
-// n = n_base + wave_n + 32 i + 8 g + 4 (lane / 32) + {0,1,2,3} in acc[i][j][4g .. 4g+3].
-// All accumulator indices are compile-time constants (static_for).
-template <int ODT, int MODE, bool GELU, int TN, int TM>
-__device__ __forceinline__ void store_tiles(const v16i (&acc)[TN][TM], int lane, int m_base,
-                                            int n_base, int wave_m, int wave_n, int M, int N,
-                                            const float* __restrict__ xs,
-                                            const float* __restrict__ ws, int64_t ws_size,
-                                            const void* __restrict__ bias, void* __restrict__ out) {
-    const int lane_m = lane % 32;
-    const int lane_n = 4 * (lane / 32);
-    float xsv[TM];
-    if constexpr (MODE == 0) {
-        static_for<0, TM>([&](auto j) {
-            const int m = m_base + wave_m + j * 32 + lane_m;
-            xsv[j] = xs[m < M ? m : M - 1];
-        });
-    }
-    const bool vec_ok = (N % 4) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
-    static_for<0, TN>([&](auto i) {
-        static_for<0, 4>([&](auto g) {
-            const int n0 = n_base + wave_n + i * 32 + 8 * g + lane_n;
-            float wsv[4], bv[4];
-            if constexpr (MODE == 0) {
-                static_for<0, 4>([&](auto e) {
-                    const int n = n0 + e < N ? n0 + e : N - 1;
-                    wsv[e] = ws[ws_size == 1 ? 0 : n];
-                    bv[e] = bias ? DType<ODT>::load(
-                                       static_cast<const typename DType<ODT>::storage*>(bias)[n])
-                                 : 0.0f;
-                });
-            }
-            static_for<0, TM>([&](auto j) {
-                const int m = m_base + wave_m + j * 32 + lane_m;
-                if (m < M) {
-                    const int64_t row = static_cast<int64_t>(m) * N;
-                    if constexpr (MODE == 1) {
-                        int32_t* o = static_cast<int32_t*>(out) + row;
-                        if (vec_ok && n0 + 3 < N) {
-                            *reinterpret_cast<v4i*>(o + n0) =
-                                v4i{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                    acc[i][j][4 * g + 3]};
-                        } else {
-                            static_for<0, 4>([&](auto e) {
-                                if (n0 + e < N) o[n0 + e] = acc[i][j][4 * g + e];
-                            });
-                        }
-                    } else {
-                        float v[4];
-                        static_for<0, 4>([&](auto e) {
-                            v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
-                        });
-                        using OS = typename DType<ODT>::storage;
-                        OS* o = static_cast<OS*>(out) + row;
-                        if (vec_ok && n0 + 3 < N) {
-                            if constexpr (ODT == W8A8_F32) {
-                                *reinterpret_cast<float4*>(o + n0) = make_float4(v[0], v[1], v[2], v[3]);
-                            } else {
-                                uint2 p;
-                                p.x = static_cast<uint32_t>(DType<ODT>::store(v[0])) |
-                                      (static_cast<uint32_t>(DType<ODT>::store(v[1])) << 16);
-                                p.y = static_cast<uint32_t>(DType<ODT>::store(v[2])) |
-                                      (static_cast<uint32_t>(DType<ODT>::store(v[3])) << 16);
-                                *reinterpret_cast<uint2*>(o + n0) = p;
-                            }
-                        } else {
-                            static_for<0, 4>([&](auto e) {
-                                if (n0 + e < N) o[n0 + e] = DType<ODT>::store(v[e]);
-                            });
-                        }
-                    }
-                }
-            });
-        });
-    });
-}
-
-template <int BN, int BM, int BK, int WN, int WM>
-struct GemmShape {
-    static constexpr int kThreads = 256;
-    static constexpr int kWaves = 4;
-    static_assert((BN / WN) * (BM / WM) == kWaves, "4 waves per block");
-    static constexpr int TN = WN / 32, TM = WM / 32;   // MFMA tiles per wave
-    static constexpr int kRow = BK + 16;                // padded LDS row, bytes
-    static constexpr int kChunksPerRow = BK / 16;
-    static constexpr int kWChunks = BN * kChunksPerRow / kThreads;   // per thread
-    static constexpr int kXChunks = BM * kChunksPerRow / kThreads;   // per thread (int8 source)
-    static constexpr int kStage = (BN + BM) * kRow;                  // bytes per LDS stage
-};
-
-// MODE: 0 = dtype output with bias (if any) and optional GELU; 1 = int32 output.
-template <int ODT, int MODE, bool GELU, int XDT, int BN, int BM, int BK, int WN, int WM>
-__global__ __launch_bounds__(256, 1) void gemm_mfma(
-    const int8_t* __restrict__ q, const void* __restrict__ xsrc, const int8_t* __restrict__ w,
-    const float* __restrict__ xs, const float* __restrict__ ws, int64_t ws_size,
-    const void* __restrict__ bias, void* __restrict__ out, int M, int N, int K, int group_m) {
-    using S = GemmShape<BN, BM, BK, WN, WM>;
-    constexpr bool XQ = XDT >= 0;          // activation quantized in the tile load
-    constexpr int XDTq = XQ ? XDT : W8A8_BF16;
-    using XD = DType<XDTq>;
-    constexpr int XE = 16 / XD::bytes;     // float elements per 16-byte source chunk (XQ)
-    constexpr int kXSrcChunksPerRow = XQ ? BK / XE : S::kChunksPerRow;
-    constexpr int kXLoads = BM * kXSrcChunksPerRow / S::kThreads;
-
-    __shared__ __attribute__((aligned(16))) int8_t lds[2 * S::kStage];
-
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n, group_m);
-    const int m_base = tc.tm * BM, n_base = tc.tn * BN;
-
-    const int t = threadIdx.x;
-    const int lane = t % kWave, wave = t / kWave;
-    const int wave_n = (wave % (BN / WN)) * WN;
-    const int wave_m = (wave / (BN / WN)) * WM;
-    const int KT = (K + BK - 1) / BK;
-
-    // ---- global -> register staging
-    uint4 wreg[S::kWChunks];
-    uint4 xreg[kXLoads];
-    // per-row quantizer constants of the rows this thread loads (XQ)
-    RowQuant xrq[XQ ? kXLoads : 1];
-    if constexpr (XQ) {
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-            const int cid = t + i * S::kThreads;
-            int m = m_base + cid / kXSrcChunksPerRow;
-            m = m < M ? m : M - 1;
-            xrq[i] = row_quant<XDTq>(xs[m]);
-        }
-    }
-
-    auto load_tile = [&](int kt) {
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < S::kWChunks; ++i) {
-            const int cid = t + i * S::kThreads;
-            const int r = cid / S::kChunksPerRow, c = cid % S::kChunksPerRow;
-            int n = n_base + r;
-            n = n < N ? n : N - 1;
-            const int k = k0 + c * 16;
-            wreg[i] = k < K ? *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(n) * K + k)
-                            : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-            const int cid = t + i * S::kThreads;
-            const int r = cid / kXSrcChunksPerRow, c = cid % kXSrcChunksPerRow;
-            int m = m_base + r;
-            m = m < M ? m : M - 1;
-            if constexpr (XQ) {
-                const int k = k0 + c * XE;
-                const char* base = static_cast<const char*>(xsrc) +
-                                   (static_cast<int64_t>(m) * K + k) * XD::bytes;
-                xreg[i] = k < K ? *reinterpret_cast<const uint4*>(base) : make_uint4(0, 0, 0, 0);
-            } else {
-                const int k = k0 + c * 16;
-                xreg[i] = k < K ? *reinterpret_cast<const uint4*>(q + static_cast<int64_t>(m) * K + k)
-                                : make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    auto store_tile = [&](int stage) {
-        int8_t* wl = lds + stage * S::kStage;
-        int8_t* xl = wl + BN * S::kRow;
-#pragma unroll
-        for (int i = 0; i < S::kWChunks; ++i) {
-            const int cid = t + i * S::kThreads;
-            const int r = cid / S::kChunksPerRow, c = cid % S::kChunksPerRow;
-            *reinterpret_cast<uint4*>(wl + r * S::kRow + c * 16) = wreg[i];
-        }
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i) {
-            const int cid = t + i * S::kThreads;
-            const int r = cid / kXSrcChunksPerRow, c = cid % kXSrcChunksPerRow;
-            if constexpr (XQ) {
-                const typename XD::storage* e = reinterpret_cast<const typename XD::storage*>(&xreg[i]);
-                int code[XE];
-#pragma unroll
-                for (int j = 0; j < XE; ++j) code[j] = quant_elem<XDTq>(XD::load(e[j]), xrq[i]);
-                if constexpr (XE == 8) {
-                    uint2 p;
-                    p.x = pack4_i8(code[0], code[1], code[2], code[3]);
-                    p.y = pack4_i8(code[4], code[5], code[6], code[7]);
-                    *reinterpret_cast<uint2*>(xl + r * S::kRow + c * 8) = p;
-                } else {
-                    *reinterpret_cast<uint32_t*>(xl + r * S::kRow + c * 4) =
-                        pack4_i8(code[0], code[1], code[2], code[3]);
-                }
-            } else {
-                *reinterpret_cast<uint4*>(xl + r * S::kRow + c * 16) = xreg[i];
-            }
-        }
-    };
-
-    v16i acc[S::TN][S::TM];
-#pragma unroll
-    for (int i = 0; i < S::TN; ++i)
-#pragma unroll
-        for (int j = 0; j < S::TM; ++j) acc[i][j] = v16i{};
-
-    if (KT > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
-
-    const int frag_row = lane % 32;
-    const int frag_k = (lane / 32) * 16;
-    for (int kt = 0; kt < KT; ++kt) {
-        const int stage = kt & 1;
-        if (kt + 1 < KT) load_tile(kt + 1);
-        const int8_t* wl = lds + stage * S::kStage;
-        const int8_t* xl = wl + BN * S::kRow;
-#pragma unroll
-        for (int ks = 0; ks < BK / 32; ++ks) {
-            v4i a[S::TN], b[S::TM];
-#pragma unroll
-            for (int i = 0; i < S::TN; ++i)
-                a[i] = *reinterpret_cast<const v4i*>(wl + (wave_n + i * 32 + frag_row) * S::kRow +
-                                                     ks * 32 + frag_k);
-#pragma unroll
-            for (int j = 0; j < S::TM; ++j)
-                b[j] = *reinterpret_cast<const v4i*>(xl + (wave_m + j * 32 + frag_row) * S::kRow +
-                                                     ks * 32 + frag_k);
-#pragma unroll
-            for (int i = 0; i < S::TN; ++i)
-#pragma unroll
-                for (int j = 0; j < S::TM; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < KT) store_tile(stage ^ 1);
-        __syncthreads();
-    }
-
-    store_tiles<ODT, MODE, GELU, S::TN, S::TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
-                                               ws_size, bias, out);
-}
-
-// ---------------------------------------------------------------- LDS-DMA main loop
-//
-// Same MFMA tiling and accumulator layout as gemm_mfma, but the K tiles travel
-// from global memory straight into LDS (global_load_lds_dwordx4: each lane
-// moves 16 bytes, a wave fills 1 KB of contiguous LDS), through a ring of
-// STAGES buffers, so no VGPRs stage the tiles and no LDS write instructions
-// are issued.  The LDS tile is unpadded (BK bytes per row).  Bank conflicts of
-// the 128-bit fragment reads are avoided by an XOR swizzle of the 16-byte
-// chunk index that depends only on row mod 32 (so it is a per-lane constant):
-//   BK =  64 (4 chunks/row): chunk' = chunk ^ (((row >> 1) ^ (row >> 3)) & 3)
-//   BK = 128 (8 chunks/row): chunk' = chunk ^ ((row & 7) ^ ((row >> 3) & 3))
-// Either makes the rows read in one LDS cycle (8 consecutive rows for a
-// 128-byte-wide LDS, 16 for a 256-byte-wide one) land in distinct banks.  The
-// swizzle is applied on the load side by choosing which global chunk each
-// lane fetches.
-//
-// Occupancy: OCC blocks of 4 waves per CU (OCC = 2 keeps each wave within 256
-// registers, 128 of them accumulators), so one block's epilogue and barrier
-// waits run under the other block's MFMAs.
-//
-// Synchronisation: one raw s_barrier per K tile, preceded by
-// s_waitcnt vmcnt(loads of later tiles) lgkmcnt(0): the wave's own DMA for
-// the tile about to be read has landed and its reads of the tile just
-// consumed have completed, so after the barrier every wave may read the new
-// tile and the buffer of the consumed one may be refilled.  The barrier is
-// crossed before the last k32 substep of a tile, so the LDS latency of the
-// next tile's first fragments hides under that substep's MFMAs.  Inside a
-// substep the fragment reads of the next substep are interleaved one by one
-// with the MFMAs (sched_group_barrier), which keeps two fragment sets live.
-//
-// Epilogue of 16-bit outputs: the block's dequantized tile is staged through
-// the (then idle) LDS ring, rows of BN values with the 16-byte chunk index
-// XOR-swizzled by the row, and leaves as full-row 16-byte-per-lane stores, so
-// every output line is written whole.
-template <int BK>
-__device__ __forceinline__ int swz(int row) {
-    if constexpr (BK == 64) return ((row >> 1) ^ (row >> 3)) & 3;
-    else return (row & 7) ^ ((row >> 3) & 3);
-}
-
-// s_waitcnt immediate for gfx9: vmcnt = n (0..63), expcnt unconstrained, lgkmcnt = 0.
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | (((N >> 4) & 3) << 14));
-}
-
-#define W8A8_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-#define W8A8_GLB_PTR(p) ((const __attribute__((address_space(1))) void*)(p))
-
-// sched_group_barrier masks
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedVmem = 0x010;
-constexpr int kSchedDsRead = 0x100;
-
-template <int BN_, int BM_, int WN_, int WM_, int BK_, int STAGES_, int OCC_>
-struct DmaCfg {
-    static constexpr int BN = BN_, BM = BM_, WN = WN_, WM = WM_, BK = BK_, STAGES = STAGES_, OCC = OCC_;
-    static_assert((BN / WN) * (BM / WM) == 4, "4 waves per block");
-    static constexpr int TN = WN / 32, TM = WM / 32;       // MFMA tiles per wave
-    static constexpr int CPR = BK / 16;                    // 16-byte chunks per LDS row
-    static constexpr int KS = BK / 32;                     // k32 substeps per tile
-    static constexpr int kTileBytes = (BN + BM) * BK;      // one stage: weights then activations
-    static constexpr int kWaveLoads = kTileBytes / 1024;   // 1 KB per wave-load
-    static_assert(kWaveLoads % 4 == 0, "wave-loads split evenly over 4 waves");
-    static constexpr int kLoadsPerThread = kWaveLoads / 4;
-    static constexpr int kWWaveLoads = BN * BK / 1024;
-    static_assert(kLoadsPerThread * (STAGES - 2) < 64, "vmcnt range");
-    static constexpr int kLds = STAGES * kTileBytes;
-    // 16-bit output tile staged through LDS for whole-line stores
-    static constexpr bool kStageOut = BN * BM * 2 <= kLds;
-};
-
-// The 16-byte output chunk c of staged row r sits at chunk c ^ (r mod chunks-per-row, up to 32).
-template <int BN>
-__device__ __forceinline__ int out_swz(int row) {
-    constexpr int kChunks = BN / 8;
-    return row & ((kChunks < 32 ? kChunks : 32) - 1);
-}
-
-// Dequantize the block's accumulators into the LDS ring as a BM x BN tile of
-// 16-bit values, then write it out row by row, 16 bytes per lane (N % 8 == 0,
-// 16-byte aligned out).  Same values as store_tiles.
-template <int ODT, bool GELU, class C>
-__device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::TM], int8_t* lds,
-                                                   int lane, int t, int m_base, int n_base,
-                                                   int wave_m, int wave_n, int M, int N,
-                                                   const float* __restrict__ xs,
-                                                   const float* __restrict__ ws, int64_t ws_size,
-                                                   const void* __restrict__ bias,
-                                                   void* __restrict__ out) {
-    constexpr int BN = C::BN, BM = C::BM, TN = C::TN, TM = C::TM;
-    constexpr int kRowBytes = BN * 2;
-    constexpr int kChunks = BN / 8;   // 16-byte chunks per staged row
-    using OS = typename DType<ODT>::storage;
-    const int lane_m = lane % 32, half = lane / 32;
-    float xsv[TM];
-    static_for<0, TM>([&](auto j) {
-        const int m = m_base + wave_m + j * 32 + lane_m;
-        xsv[j] = xs[m < M ? m : M - 1];
-    });
-    __syncthreads();  // every wave has finished reading the last K tile
-    static_for<0, TN>([&](auto i) {
-        static_for<0, 4>([&](auto g) {
-            const int chunk = (wave_n + i * 32 + 8 * g) / 8;
-            const int n0 = n_base + wave_n + i * 32 + 8 * g + 4 * half;
-            float wsv[4], bv[4];
-            static_for<0, 4>([&](auto e) {
-                const int n = n0 + e < N ? n0 + e : N - 1;
-                wsv[e] = ws[ws_size == 1 ? 0 : n];
-                bv[e] = bias ? DType<ODT>::load(static_cast<const OS*>(bias)[n]) : 0.0f;
-            });
-            static_for<0, TM>([&](auto j) {
-                const int ml = wave_m + j * 32 + lane_m;
-                float v[4];
-                static_for<0, 4>([&](auto e) {
-                    v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
-                });
-                uint2 p;
-                p.x = static_cast<uint32_t>(DType<ODT>::store(v[0])) |
-                      (static_cast<uint32_t>(DType<ODT>::store(v[1])) << 16);
-                p.y = static_cast<uint32_t>(DType<ODT>::store(v[2])) |
-                      (static_cast<uint32_t>(DType<ODT>::store(v[3])) << 16);
-                *reinterpret_cast<uint2*>(lds + ml * kRowBytes + (chunk ^ out_swz<BN>(ml)) * 16 + half * 8) = p;
-            });
-        });
-    });
-    __syncthreads();
-    constexpr int kTotal = BM * kChunks;
-    static_assert(kTotal % 256 == 0, "whole passes of 256 chunks");
-#pragma unroll 4
-    for (int pass = 0; pass < kTotal / 256; ++pass) {
-        const int idx = pass * 256 + t;
-        const int r = idx / kChunks, c = idx % kChunks;
-        const int m = m_base + r, n = n_base + c * 8;
-        const uint4 v = *reinterpret_cast<const uint4*>(lds + r * kRowBytes + (c ^ out_swz<BN>(r)) * 16);
-        if (m < M && n < N) *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
-    }
-}
-
-template <int ODT, int MODE, bool GELU, class C>
-__global__ __launch_bounds__(256, C::OCC) void gemm_mfma_dma(
-    const int8_t* __restrict__ q, const int8_t* __restrict__ w, const float* __restrict__ xs,
-    const float* __restrict__ ws, int64_t ws_size, const void* __restrict__ bias,
-    void* __restrict__ out, int M, int N, int K, int group_m) {
-    constexpr int BN = C::BN, BM = C::BM, WN = C::WN, WM = C::WM, BK = C::BK, STAGES = C::STAGES;
-    constexpr int TN = C::TN, TM = C::TM, CPR = C::CPR, KS = C::KS;
-    constexpr int kTileBytes = C::kTileBytes, kLoadsPerThread = C::kLoadsPerThread;
-    constexpr int kWWaveLoads = C::kWWaveLoads;
-    __shared__ __attribute__((aligned(1024))) int8_t lds[C::kLds];
-
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n, group_m);
-    const int m_base = tc.tm * BM, n_base = tc.tn * BN;
-    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
-    const int wave_n = (wave % (BN / WN)) * WN;
-    const int wave_m = (wave / (BN / WN)) * WM;
-    const int KT = K / BK;                                 // K % BK == 0 (host checks)
-
-    // Source of each wave-load this lane takes part in: wave-load L (global
-    // index wave * kLoadsPerThread + j) fills LDS chunks [64 L, 64 L + 64) of the
-    // stage; chunk p holds row p / CPR, logical chunk (p % CPR) ^ swz(row).
-    const int8_t* src[kLoadsPerThread];
-#pragma unroll
-    for (int j = 0; j < kLoadsPerThread; ++j) {
-        const int L = wave * kLoadsPerThread + j;
-        const bool is_w = L < kWWaveLoads;
-        const int p = (is_w ? L : L - kWWaveLoads) * 64 + lane;
-        const int r = p / CPR;
-        const int c = (p % CPR) ^ swz<BK>(r);
-        int row = (is_w ? n_base : m_base) + r;
-        const int lim = is_w ? N : M;
-        row = row < lim ? row : lim - 1;
-        src[j] = (is_w ? w : q) + static_cast<int64_t>(row) * K + c * 16;
-    }
-    auto issue = [&](int kt, int stage) {
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int j = 0; j < kLoadsPerThread; ++j) {
-            const int L = wave * kLoadsPerThread + j;
-            __builtin_amdgcn_global_load_lds(W8A8_GLB_PTR(src[j] + k0),
-                                             W8A8_LDS_PTR(lds + stage * kTileBytes + L * 1024), 16, 0, 0);
-        }
-    };
-
-    v16i acc[TN][TM];
-#pragma unroll
-    for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = v16i{};
-
-    const int fl = swz<BK>(lane % 32);
-    int rd[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) rd[ks] = (((2 * ks + lane / 32) ^ fl) * 16);
-    const int wrow = (wave_n + lane % 32) * BK;
-    const int xrow = (BN + wave_m + lane % 32) * BK;
-
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-        if (s < KT) issue(s, s);
-
-    // Fragments of one k32 substep: TN weight fragments, TM activation fragments.
-    auto read_frags = [&](int stage, int ks, v4i (&a)[TN], v4i (&b)[TM]) {
-        const int8_t* base = lds + stage * kTileBytes + rd[ks];
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-            a[i] = *reinterpret_cast<const v4i*>(base + wrow + i * 32 * BK);
-#pragma unroll
-        for (int j = 0; j < TM; ++j)
-            b[j] = *reinterpret_cast<const v4i*>(base + xrow + j * 32 * BK);
-    };
-    auto mfmas = [&](const v4i (&a)[TN], const v4i (&b)[TM]) {
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-            for (int j = 0; j < TM; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-    };
-    // One MFMA, then one fragment read, while reads remain; then the rest of
-    // the MFMAs.
-    auto interleave = [&]() {
-        constexpr int kReads = TN + TM, kMfma = TN * TM;
-        constexpr int kPairs = kReads < kMfma ? kReads : kMfma;
-        static_for<0, kPairs>([&](auto) {
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-        });
-        if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(kSchedMfma, kMfma - kPairs, 0);
-        if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReads - kPairs, 0);
-    };
-    // Wait until this wave's DMA for the next tile has landed (at most `after`
-    // later tiles still in flight) and its LDS reads have completed.
-    auto wait_tile = [&](int after) {
-        if constexpr (STAGES >= 4) {
-            if (after >= 2) { wait_vm_lgkm0<2 * kLoadsPerThread>(); return; }
-        }
-        if constexpr (STAGES >= 3) {
-            if (after >= 1) { wait_vm_lgkm0<kLoadsPerThread>(); return; }
-        }
-        wait_vm_lgkm0<0>();
-    };
-
-    v4i fa[2][TN], fb[2][TM];   // two fragment sets, alternating by substep parity
-    if (KT > 0) {
-        wait_tile(KT - 1 < STAGES - 2 ? KT - 1 : STAGES - 2);
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        if (STAGES - 1 < KT) issue(STAGES - 1, STAGES - 1);
-        read_frags(0, 0, fa[0], fb[0]);
-    }
-    int stage = 0;
-    for (int kt = 0; kt < KT; ++kt) {
-        const int next = stage + 1 == STAGES ? 0 : stage + 1;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int cur = ks & 1;
-            if (ks + 1 < KS) {
-                read_frags(stage, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
-            } else {
-                if (kt + 1 < KT) {
-                    // tiles issued so far: up to min(KT - 1, kt + STAGES - 1)
-                    const int last = KT - 1 < kt + STAGES - 1 ? KT - 1 : kt + STAGES - 1;
-                    wait_tile(last - (kt + 1));
-                    __builtin_amdgcn_s_barrier();
-                    __builtin_amdgcn_sched_barrier(0);
-                    if (kt + STAGES < KT) issue(kt + STAGES, stage);
-                }
-                // first fragments of the next tile (after the last tile: an
-                // unused in-bounds read, which keeps this one basic block)
-                read_frags(next, 0, fa[cur ^ 1], fb[cur ^ 1]);
-            }
-            // The single MFMA block of the substep: one copy only, so the
-            // accumulators stay in AGPRs.
-            mfmas(fa[cur], fb[cur]);
-            interleave();
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        stage = next;
-    }
-
-    if constexpr (MODE == 0 && ODT != W8A8_F32 && C::kStageOut) {
-        const bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
-        if (vec_ok) {
-            store_tiles_staged<ODT, GELU, C>(acc, lds, lane, t, m_base, n_base, wave_m, wave_n, M, N,
-                                             xs, ws, ws_size, bias, out);
-            return;
-        }
-    }
-    store_tiles<ODT, MODE, GELU, TN, TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
-                                         ws_size, bias, out);
-}
-
-// Generic GEMM for shapes the MFMA kernel does not take (K % 16 != 0,
-// unaligned operands, fused quant of fp32 inputs): one thread per output.
-template <int ODT, int MODE, bool GELU>
-__global__ __launch_bounds__(256) void gemm_generic(const int8_t* __restrict__ q,
-                                                    const int8_t* __restrict__ w,
-                                                    const float* __restrict__ xs,
-                                                    const float* __restrict__ ws, int64_t ws_size,
-                                                    const void* __restrict__ bias,
-                                                    void* __restrict__ out, int64_t M, int64_t N,
-                                                    int64_t K) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= M * N) return;
-    const int64_t m = idx / N, n = idx % N;
-    int acc = 0;
-    for (int64_t k = 0; k < K; ++k) acc += static_cast<int>(q[m * K + k]) * static_cast<int>(w[n * K + k]);
-    if constexpr (MODE == 1) {
-        static_cast<int32_t*>(out)[idx] = acc;
-    } else {
-        const float b = bias ? DType<ODT>::load(static_cast<const typename DType<ODT>::storage*>(bias)[n]) : 0.0f;
-        static_cast<typename DType<ODT>::storage*>(out)[idx] =
-            DType<ODT>::store(epilogue_value<ODT>(acc, xs[m], ws[ws_size == 1 ? 0 : n], b, GELU));
-    }
-}
-
-// Standalone dequant of int32 accumulators (the reference's cuBLAS route's
-// second kernel, int8_linear.cu:517-583).
-template <int ODT, bool GELU>
-__global__ __launch_bounds__(256) void dequant_linear(const int32_t* __restrict__ acc,
-                                                      const float* __restrict__ xs,
-                                                      const float* __restrict__ ws, int64_t ws_size,
-                                                      const void* __restrict__ bias,
-                                                      void* __restrict__ out, int64_t M, int64_t N) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= M * N) return;
-    const int64_t m = idx / N, n = idx % N;
-    const float b = bias ? DType<ODT>::load(static_cast<const typename DType<ODT>::storage*>(bias)[n]) : 0.0f;
-    static_cast<typename DType<ODT>::storage*>(out)[idx] =
-        DType<ODT>::store(epilogue_value<ODT>(acc[idx], xs[m], ws[ws_size == 1 ? 0 : n], b, GELU));
-}
 
 // ------------------------------------------------------------------ host side
 
@@ -648,23 +30,39 @@ bool gemm_mfma_supported(const void* a, size_t a_elem, const int8_t* w, int64_t 
 }
 
 // Main-loop configurations of the int8-input GEMM (weights BN x activations BM
-// per block, wave tile WN x WM, BK bytes per K tile, ring depth, blocks per CU).
+// per block, wave tile WN x WM, BK bytes per K tile, ring depth, waves per SIMD).
+//   N256M256W8: 8 waves of 128 x 64 on a 256 x 256 tile, 2-stage ring of
+//               128-byte K tiles (128 KB of LDS), one block per CU.  The default.
+//   N256M128:   4 waves of 128 x 64 on a 256 x 128 tile, 3-stage ring of 64-byte
+//               K tiles (72 KB), two blocks per CU.
+//   N256M256:   4 waves of 128 x 128, 2-stage ring of 128-byte tiles, one wave
+//               per SIMD.
+using CfgN256M256W8 = DmaCfg<256, 256, 128, 64, 128, 2, 2>;
 using CfgN256M128 = DmaCfg<256, 128, 128, 64, 64, 3, 2>;
-using CfgN128M256 = DmaCfg<128, 256, 64, 128, 64, 3, 2>;
 using CfgN256M256 = DmaCfg<256, 256, 128, 128, 128, 2, 1>;
 
-// W8A8_GEMM_MAINLOOP = n256m128 | n128m256 | n256m256 | regs selects one (a
+// W8A8_GEMM_MAINLOOP = n256m256w8 | n256m128 | n256m256 | regs selects one (a
 // tuning knob; every choice produces identical results).
 static int mainloop_choice() {
     static int choice = [] {
         const char* e = std::getenv("W8A8_GEMM_MAINLOOP");
-        if (!e) return 1;
+        if (!e) return 4;
         if (std::strcmp(e, "regs") == 0) return 0;
-        if (std::strcmp(e, "n128m256") == 0) return 2;
+        if (std::strcmp(e, "n256m128") == 0) return 1;
         if (std::strcmp(e, "n256m256") == 0) return 3;
-        return 1;
+        return 4;
     }();
     return choice;
+}
+
+// W8A8_GEMM_GLOBAL_LOADS=1 forces the global_load_lds form (tuning knob;
+// identical results).
+static bool buffer_loads_disabled() {
+    static bool off = [] {
+        const char* e = std::getenv("W8A8_GEMM_GLOBAL_LOADS");
+        return e && e[0] == '1';
+    }();
+    return off;
 }
 
 template <int ODT, int MODE, bool GELU, class C>
@@ -672,9 +70,16 @@ static void launch_dma(const int8_t* q, const int8_t* w, const float* xs, const 
                        int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
                        hipStream_t stream) {
     const int tiles = static_cast<int>(((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN));
-    hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C>), dim3(tiles), dim3(256), 0, stream,
-                       q, w, xs, ws, ws_size, bias, out, static_cast<int>(M), static_cast<int>(N),
-                       static_cast<int>(K), kGroupM);
+    // buffer-resource loads take 32-bit offsets: both operands below 2 GiB
+    const int64_t kBufLimit = (1ll << 31) - 4096;
+    if (M * K < kBufLimit && N * K < kBufLimit && !buffer_loads_disabled())
+        hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C, true>), dim3(tiles), dim3(C::kThreads), 0, stream,
+                           q, w, xs, ws, ws_size, bias, out, static_cast<int>(M), static_cast<int>(N),
+                           static_cast<int>(K), kGroupM);
+    else
+        hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C, false>), dim3(tiles), dim3(C::kThreads), 0, stream,
+                           q, w, xs, ws, ws_size, bias, out, static_cast<int>(M), static_cast<int>(N),
+                           static_cast<int>(K), kGroupM);
 }
 
 template <int ODT, int MODE, bool GELU>
@@ -684,14 +89,16 @@ static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const flo
     const int choice = mainloop_choice();
     // whole K tiles only (the DMA ring has no tail masking)
     if (choice == 0) return false;
-    if (choice == 3) {
-        if (K % CfgN256M256::BK != 0) return false;
+    if (choice == 4 && K % CfgN256M256W8::BK == 0) {
+        launch_dma<ODT, MODE, GELU, CfgN256M256W8>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+        return true;
+    }
+    if (choice == 3 && K % CfgN256M256::BK == 0) {
         launch_dma<ODT, MODE, GELU, CfgN256M256>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
         return true;
     }
-    if (K % 64 != 0) return false;
-    if (choice == 2) launch_dma<ODT, MODE, GELU, CfgN128M256>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
-    else launch_dma<ODT, MODE, GELU, CfgN256M128>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+    if (K % CfgN256M128::BK != 0) return false;
+    launch_dma<ODT, MODE, GELU, CfgN256M128>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
     return true;
 }
 
@@ -700,12 +107,14 @@ static void gemm_dispatch_odt(const int8_t* q, const int8_t* w, const float* xs,
                               int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N,
                               int64_t K, bool int32_out, hipStream_t stream) {
     const bool fast = gemm_mfma_supported(q, 1, w, M, N, K);
-    if (int32_out) {
-        if (fast && try_dma<ODT, 1, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream)) return;
-        if (fast) launch_mfma<ODT, 1, false, -1>(q, nullptr, w, xs, ws, ws_size, bias, out, M, N, K, stream);
-        else hipLaunchKernelGGL((gemm_generic<ODT, 1, false>), dim3(static_cast<unsigned>((M * N + 255) / 256)),
-                                dim3(256), 0, stream, q, w, xs, ws, ws_size, bias, out, M, N, K);
-        return;
+    if constexpr (ODT == W8A8_F32 && !GELU) {   // the int32 mode is instantiated once
+        if (int32_out) {
+            if (fast && try_dma<ODT, 1, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream)) return;
+            if (fast) launch_mfma<ODT, 1, false, -1>(q, nullptr, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+            else hipLaunchKernelGGL((gemm_generic<ODT, 1, false>), dim3(static_cast<unsigned>((M * N + 255) / 256)),
+                                    dim3(256), 0, stream, q, w, xs, ws, ws_size, bias, out, M, N, K);
+            return;
+        }
     }
     if (fast && try_dma<ODT, 0, GELU>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream)) return;
     if (fast) launch_mfma<ODT, 0, GELU, -1>(q, nullptr, w, xs, ws, ws_size, bias, out, M, N, K, stream);
@@ -716,10 +125,14 @@ static void gemm_dispatch_odt(const int8_t* q, const int8_t* w, const float* xs,
 void launch_gemm(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                  int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
                  int64_t K, bool gelu, bool int32_out, hipStream_t stream) {
+    if (int32_out) {
+        gemm_dispatch_odt<W8A8_F32, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, true, stream);
+        return;
+    }
 #define W8A8_GEMM_CASE(ODT)                                                                       \
     if (out_dtype == ODT) {                                                                       \
-        if (gelu && !int32_out) gemm_dispatch_odt<ODT, true>(q, w, xs, ws, ws_size, bias, out, M, N, K, false, stream); \
-        else gemm_dispatch_odt<ODT, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, int32_out, stream); \
+        if (gelu) gemm_dispatch_odt<ODT, true>(q, w, xs, ws, ws_size, bias, out, M, N, K, false, stream); \
+        else gemm_dispatch_odt<ODT, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, false, stream); \
         return;                                                                                   \
     }
     W8A8_GEMM_CASE(W8A8_BF16)
