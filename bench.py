@@ -235,14 +235,35 @@ def main():
                    "ffn": FFN, "linears": "qkv 3072->9216, out 3072->3072, up 3072->12288 +gelu_tanh, "
                                          "down 12288->3072; per-token quant of each input included",
                    "parallelism": "single_gpu", "pct_int8_peak": round(100 * value / PEAK_INT8_TOPS, 2)},
-        "roofline": {"kernel": "gemm_mfma (FFN-up 11712x3072x12288, bf16 out, GELU epilogue)",
+        "roofline": {"kernel": "gemm_mfma_dma DmaCfg<256,192,64,96,128,2,2> (FFN-up 11712x3072x12288, "
+                               "bf16 out, GELU epilogue)",
                      "bound": "mfma", "achieved": round(up_tops, 2), "peak": PEAK_INT8_TOPS,
-                     "unit": "TOPS", "frac": round(up_tops / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "unit": "TOPS", "frac": round(up_tops / PEAK_INT8_TOPS, 4), "traffic": traffic_bytes(),
                      "launch_us": round(up_ms * 1e3, 2), "algorithmic_ops": up_ops},
         "cpu_baseline": cpu,
         "extras": extras,
     }
     print(json.dumps(line), flush=True)
+
+
+def traffic_bytes():
+    """HBM bytes per launch of the roofline kernel, read from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the same kernel and workload
+    (profiles/), or None when a tuning knob selects another main loop than the
+    one profiled."""
+    if os.environ.get("W8A8_GEMM_MAINLOOP") or os.environ.get("W8A8_GEMM_GLOBAL_LOADS"):
+        return None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "hbm_traffic_ffn_up_gemm_and_quant_M11712.txt")
+    key = "gemm_mfma_dma DmaCfg<256,192,64,96,128,2,2> ffn_up traffic_bytes_per_launch:"
+    try:
+        with open(path) as f:
+            for line in f:
+                if key in line:
+                    return int(line.split(key, 1)[1].split()[0])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv):

@@ -31,26 +31,33 @@ bool gemm_mfma_supported(const void* a, size_t a_elem, const int8_t* w, int64_t 
 
 // Main-loop configurations of the int8-input GEMM (weights BN x activations BM
 // per block, wave tile WN x WM, BK bytes per K tile, ring depth, waves per SIMD).
+//   N256M192W8: 8 waves of 64 x 96 on a 256 x 192 tile, 2-stage ring of
+//               128-byte K tiles (112 KB of LDS), one block per CU.  The
+//               default: 192-token tiles cut M = 11712 (2 x 5856) exactly and
+//               fill the 256 CUs in rounds that are ~95% full at N = 3072,
+//               9216 and 12288.
 //   N256M256W8: 8 waves of 128 x 64 on a 256 x 256 tile, 2-stage ring of
-//               128-byte K tiles (128 KB of LDS), one block per CU.  The default.
+//               128-byte K tiles (128 KB of LDS), one block per CU.
 //   N256M128:   4 waves of 128 x 64 on a 256 x 128 tile, 3-stage ring of 64-byte
 //               K tiles (72 KB), two blocks per CU.
 //   N256M256:   4 waves of 128 x 128, 2-stage ring of 128-byte tiles, one wave
 //               per SIMD.
+using CfgN256M192W8 = DmaCfg<256, 192, 64, 96, 128, 2, 2>;
 using CfgN256M256W8 = DmaCfg<256, 256, 128, 64, 128, 2, 2>;
 using CfgN256M128 = DmaCfg<256, 128, 128, 64, 64, 3, 2>;
 using CfgN256M256 = DmaCfg<256, 256, 128, 128, 128, 2, 1>;
 
-// W8A8_GEMM_MAINLOOP = n256m256w8 | n256m128 | n256m256 | regs selects one (a
-// tuning knob; every choice produces identical results).
+// W8A8_GEMM_MAINLOOP = n256m192w8 | n256m256w8 | n256m128 | n256m256 | regs
+// selects one (a tuning knob; every choice produces identical results).
 static int mainloop_choice() {
     static int choice = [] {
         const char* e = std::getenv("W8A8_GEMM_MAINLOOP");
-        if (!e) return 4;
+        if (!e) return 5;
         if (std::strcmp(e, "regs") == 0) return 0;
         if (std::strcmp(e, "n256m128") == 0) return 1;
         if (std::strcmp(e, "n256m256") == 0) return 3;
-        return 4;
+        if (std::strcmp(e, "n256m256w8") == 0) return 4;
+        return 5;
     }();
     return choice;
 }
@@ -89,6 +96,10 @@ static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const flo
     const int choice = mainloop_choice();
     // whole K tiles only (the DMA ring has no tail masking)
     if (choice == 0) return false;
+    if (choice == 5 && K % CfgN256M192W8::BK == 0) {
+        launch_dma<ODT, MODE, GELU, CfgN256M192W8>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+        return true;
+    }
     if (choice == 4 && K % CfgN256M256W8::BK == 0) {
         launch_dma<ODT, MODE, GELU, CfgN256M256W8>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
         return true;

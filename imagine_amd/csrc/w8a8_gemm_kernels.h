@@ -303,6 +303,8 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma(
 // chunk index that depends only on row mod 32 (so it is a per-lane constant):
 //   BK =  64 (4 chunks/row): chunk' = chunk ^ (((row >> 1) ^ (row >> 3)) & 3)
 //   BK = 128 (8 chunks/row): chunk' = chunk ^ ((row & 7) ^ ((row >> 3) & 3))
+//   BK =  96 (6 chunks/row): no swizzle; rows start 24 banks apart, so any 8
+//                            consecutive rows read at one chunk are distinct
 // Either makes the rows read in one LDS cycle (8 consecutive rows for a
 // 128-byte-wide LDS, 16 for a 256-byte-wide one) land in distinct banks.  The
 // swizzle is applied on the load side by choosing which global chunk each
@@ -331,7 +333,8 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma(
 template <int BK>
 __device__ __forceinline__ int swz(int row) {
     if constexpr (BK == 64) return ((row >> 1) ^ (row >> 3)) & 3;
-    else return (row & 7) ^ ((row >> 3) & 3);
+    else if constexpr (BK == 128) return (row & 7) ^ ((row >> 3) & 3);
+    else return 0;   // BK = 96: the 96-byte pitch alone spreads 8 rows over distinct banks
 }
 
 // s_waitcnt immediate for gfx9: vmcnt = n (0..63), expcnt unconstrained, lgkmcnt = 0.
@@ -381,6 +384,7 @@ struct DmaCfg {
     static constexpr int kLoadsPerThread = kWaveLoads / kWaves;
     static constexpr int kWWaveLoads = BN * BK / 1024;
     static_assert(kLoadsPerThread * (STAGES - 2) < 64, "vmcnt range");
+    static_assert(BK == 64 || BK == 96 || BK == 128, "K tile of 64, 96 or 128 bytes");
     static constexpr int kLds = STAGES * kTileBytes;
     // 16-bit output tile staged through LDS for whole-line stores
     static constexpr bool kStageOut = BN * BM * 2 <= kLds;
@@ -554,15 +558,13 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
         if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReads - kPairs, 0);
     };
     // Wait until this wave's DMA for the next tile has landed (at most `after`
-    // later tiles still in flight) and its LDS reads have completed.
+    // later tiles, 0 <= after <= STAGES - 2, still in flight) and its LDS reads
+    // have completed.
     auto wait_tile = [&](int after) {
-        if constexpr (STAGES >= 4) {
-            if (after >= 2) { wait_vm_lgkm0<2 * kLoadsPerThread>(); return; }
-        }
-        if constexpr (STAGES >= 3) {
-            if (after >= 1) { wait_vm_lgkm0<kLoadsPerThread>(); return; }
-        }
-        wait_vm_lgkm0<0>();
+        static_for<0, STAGES - 1>([&](auto a) {
+            constexpr int A = decltype(a)::value;
+            if (after == A) wait_vm_lgkm0<A * kLoadsPerThread>();
+        });
     };
 
     v4i fa[2][TN], fb[2][TM];   // two fragment sets, alternating by substep parity
@@ -573,13 +575,16 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
         if (STAGES - 1 < KT) issue(STAGES - 1, STAGES - 1);
         read_frags(0, 0, fa[0], fb[0]);
     }
-    int stage = 0;
-    for (int kt = 0; kt < KT; ++kt) {
-        const int next = stage + 1 == STAGES ? 0 : stage + 1;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int cur = ks & 1;
-            if (ks + 1 < KS) {
+    // One K tile.  The fragment set of substep ks is fa/fb[(ks + P) & 1]; with an
+    // odd number of substeps per tile the parity flips from tile to tile, so
+    // tiles are then processed in pairs (P = 0, 1) to keep every register index
+    // a compile-time constant.
+    auto tile = [&](int kt, int stage, int next, auto par) {
+        constexpr int P = decltype(par)::value;
+        static_for<0, KS>([&](auto ks_) {
+            constexpr int ks = decltype(ks_)::value;
+            constexpr int cur = (ks + P) & 1;
+            if constexpr (ks + 1 < KS) {
                 read_frags(stage, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
             } else {
                 if (kt + 1 < KT) {
@@ -599,8 +604,25 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
             mfmas(fa[cur], fb[cur]);
             interleave();
             __builtin_amdgcn_sched_barrier(0);
+        });
+    };
+    auto next_stage = [](int st) { return st + 1 == STAGES ? 0 : st + 1; };
+    int stage = 0;
+    if constexpr (KS % 2 == 0) {
+        for (int kt = 0; kt < KT; ++kt) {
+            const int next = next_stage(stage);
+            tile(kt, stage, next, std::integral_constant<int, 0>{});
+            stage = next;
         }
-        stage = next;
+    } else {
+        int kt = 0;
+        for (; kt + 1 < KT; kt += 2) {
+            const int s1 = next_stage(stage), s2 = next_stage(s1);
+            tile(kt, stage, s1, std::integral_constant<int, 0>{});
+            tile(kt + 1, s1, s2, std::integral_constant<int, 1>{});
+            stage = s2;
+        }
+        if (kt < KT) tile(kt, stage, next_stage(stage), std::integral_constant<int, 0>{});
     }
 
     if constexpr (MODE == 0 && ODT != W8A8_F32 && C::kStageOut) {
