@@ -187,6 +187,31 @@ __device__ __forceinline__ int quant_elem(float x, const RowQuant& rq) {
     return static_cast<int>(v);
 }
 
+// The same code as an int8 in the low byte of the result (upper bits are
+// garbage): clamp first, then add 1.5 * 2^23, whose round-to-nearest-even
+// leaves rint(v) in the low mantissa bits (two's complement, since 2^22 sits
+// above them).  Equal to quant_elem for every non-NaN quotient (checked over
+// all 2^32 floats; clamping before rounding is exact because the clamp
+// bounds are integers), and NaN clamps to -128 in both forms.
+template <int DT>
+__device__ __forceinline__ uint32_t quant_byte(float x, const RowQuant& rq) {
+    float quot;
+    if constexpr (DT == W8A8_F32) {
+        quot = x / rq.d;
+    } else {
+        quot = DType<DT>::round(div_rn(x, rq));
+    }
+    const float v = fminf(fmaxf(quot, -128.0f), 127.0f);
+    return __float_as_uint(v + 12582912.0f);
+}
+
+// Pack the low bytes of four quant_byte results (a lowest).
+__device__ __forceinline__ uint32_t pack4_low_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);   // bytes: a0, b0, 0, 0
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x04000c0cu);   // bytes: 0, 0, c0, d0
+    return ab | cd;
+}
+
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
     return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
            ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);

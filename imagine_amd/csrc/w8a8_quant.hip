@@ -6,8 +6,8 @@
 //   s = max(amax / 127, 1e-30);  q = clamp(rint(T(x / T(s))), -128, 127)
 //
 // Bandwidth kernel.  A row is held in registers between its two passes (the
-// reference re-reads it from memory): 1 wave per row up to 512 16-byte chunks
-// (K = 4096 for 16-bit inputs), 4 waves per row up to 2048 chunks; each lane
+// reference re-reads it from memory): 1 wave per row up to 128 16-byte chunks
+// (K = 1024 for 16-bit inputs), 4 waves per row up to 2048 chunks; each lane
 // issues 128-bit loads, the absmax is a wave64 butterfly (plus a 4-entry LDS
 // exchange for 4-wave rows), and the int8 codes leave as 64-bit stores.
 // Rows that do not fit, or unaligned operands, take the generic kernel.
@@ -15,71 +15,102 @@
 
 namespace w8a8 {
 
-template <int DT, int W, int CPL, bool GELU, bool SCALES_ONLY>
+// W waves per row (1 or 4), CPL 16-byte chunks per lane, RPW rows per wave
+// group (the dispatch uses 1: two rows per wave measured slower at the DiT
+// shapes).  Every load of the group's rows is issued before any arithmetic,
+// and the rows stay in registers as raw 16-bit data (converted again in the
+// quantize pass, one shift each).
+template <int DT, int W, int CPL, int RPW, bool GELU, bool SCALES_ONLY>
 __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ xv,
                                                       int8_t* __restrict__ q,
                                                       float* __restrict__ xs, int64_t M,
                                                       int64_t K, int recip) {
     using D = DType<DT>;
     constexpr int E = 16 / D::bytes;          // elements per 16-byte chunk
-    constexpr int ROWS = 4 / W;               // rows per 256-thread block
+    constexpr int GROUPS = 4 / W;             // wave groups per 256-thread block
     const int tid = threadIdx.x % (kWave * W);
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS + threadIdx.x / (kWave * W);
+    const int grp = threadIdx.x / (kWave * W);
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * GROUPS + grp) * RPW;
     const int64_t nchunks = K / E;
-    __shared__ float wave_amax[4];
+    __shared__ float wave_amax[RPW][4];
 
-    const bool row_ok = row < M;
-    const uint4* src = reinterpret_cast<const uint4*>(
-        static_cast<const char*>(xv) + (row_ok ? row : 0) * K * D::bytes);
-
-    float v[CPL][E];
-    float amax = 0.0f;
+    uint4 raw[RPW][CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int64_t c = tid + static_cast<int64_t>(j) * kWave * W;
-        uint4 raw = make_uint4(0, 0, 0, 0);
-        if (row_ok && c < nchunks) raw = src[c];
-        const typename D::storage* e = reinterpret_cast<const typename D::storage*>(&raw);
+    for (int r = 0; r < RPW; ++r) {
+        const bool row_ok = row0 + r < M;
+        const uint4* src = reinterpret_cast<const uint4*>(
+            static_cast<const char*>(xv) + (row_ok ? row0 + r : 0) * K * D::bytes);
 #pragma unroll
-        for (int i = 0; i < E; ++i) {
-            float f = D::load(e[i]);
-            if constexpr (GELU) f = D::round(gelu_tanh(f));
-            v[j][i] = f;
-            amax = fmaxf(amax, fabsf(f));
+        for (int j = 0; j < CPL; ++j) {
+            const int64_t c = tid + static_cast<int64_t>(j) * kWave * W;
+            raw[r][j] = (row_ok && c < nchunks) ? src[c] : make_uint4(0, 0, 0, 0);
         }
     }
-    amax = wave_max(amax);
+    auto elem = [&](int r, int j, int i) {
+        const typename D::storage* e = reinterpret_cast<const typename D::storage*>(&raw[r][j]);
+        float f = D::load(e[i]);
+        if constexpr (GELU) f = D::round(gelu_tanh(f));
+        return f;
+    };
+
+    float amax[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int i = 0; i < E; ++i) m = fmaxf(m, fabsf(elem(r, j, i)));
+        amax[r] = wave_max(m);
+    }
     if constexpr (W > 1) {
         const int wave = threadIdx.x / kWave;
-        if ((threadIdx.x % kWave) == 0) wave_amax[wave] = amax;
+        if ((threadIdx.x % kWave) == 0) {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) wave_amax[r][wave] = amax[r];
+        }
         __syncthreads();
-        const int first = (threadIdx.x / (kWave * W)) * W;
+        const int first = grp * W;
 #pragma unroll
-        for (int w = 0; w < W; ++w) amax = fmaxf(amax, wave_amax[first + w]);
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int w = 0; w < W; ++w) amax[r] = fmaxf(amax[r], wave_amax[r][first + w]);
     }
-    if (!row_ok) return;
-    const float s = row_scale<DT>(amax, recip != 0);
-    if (tid == 0) xs[row] = s;
-    if constexpr (SCALES_ONLY) return;
 
-    const RowQuant rq = row_quant<DT>(s);
-    int8_t* dst = q + row * K;
+    // The quantize pass converts the raw 16-bit data again: the empty asm makes
+    // the registers opaque, so the compiler cannot keep every converted float
+    // of the absmax pass alive (which would cost the occupancy the loads need).
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const int64_t c = tid + static_cast<int64_t>(j) * kWave * W;
-        if (c >= nchunks) break;
-        if constexpr (E == 8) {
-            uint2 packed;
-            packed.x = pack4_i8(quant_elem<DT>(v[j][0], rq), quant_elem<DT>(v[j][1], rq),
-                                quant_elem<DT>(v[j][2], rq), quant_elem<DT>(v[j][3], rq));
-            packed.y = pack4_i8(quant_elem<DT>(v[j][4], rq), quant_elem<DT>(v[j][5], rq),
-                                quant_elem<DT>(v[j][6], rq), quant_elem<DT>(v[j][7], rq));
-            *reinterpret_cast<uint2*>(dst + c * E) = packed;
-        } else {
-            uint32_t packed =
-                pack4_i8(quant_elem<DT>(v[j][0], rq), quant_elem<DT>(v[j][1], rq),
-                         quant_elem<DT>(v[j][2], rq), quant_elem<DT>(v[j][3], rq));
-            *reinterpret_cast<uint32_t*>(dst + c * E) = packed;
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            asm volatile("" : "+v"(raw[r][j].x), "+v"(raw[r][j].y), "+v"(raw[r][j].z), "+v"(raw[r][j].w));
+
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int64_t row = row0 + r;
+        if (row >= M) break;
+        const float s = row_scale<DT>(amax[r], recip != 0);
+        if (tid == 0) xs[row] = s;
+        if constexpr (SCALES_ONLY) continue;
+        const RowQuant rq = row_quant<DT>(s);
+        int8_t* dst = q + row * K;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int64_t c = tid + static_cast<int64_t>(j) * kWave * W;
+            if (c >= nchunks) break;
+            if constexpr (E == 8) {
+                uint2 packed;
+                packed.x = pack4_low_bytes(quant_byte<DT>(elem(r, j, 0), rq), quant_byte<DT>(elem(r, j, 1), rq),
+                                           quant_byte<DT>(elem(r, j, 2), rq), quant_byte<DT>(elem(r, j, 3), rq));
+                packed.y = pack4_low_bytes(quant_byte<DT>(elem(r, j, 4), rq), quant_byte<DT>(elem(r, j, 5), rq),
+                                           quant_byte<DT>(elem(r, j, 6), rq), quant_byte<DT>(elem(r, j, 7), rq));
+                *reinterpret_cast<uint2*>(dst + c * E) = packed;
+            } else {
+                *reinterpret_cast<uint32_t*>(dst + c * E) =
+                    pack4_low_bytes(quant_byte<DT>(elem(r, j, 0), rq), quant_byte<DT>(elem(r, j, 1), rq),
+                                    quant_byte<DT>(elem(r, j, 2), rq), quant_byte<DT>(elem(r, j, 3), rq));
+            }
         }
     }
 }
@@ -115,28 +146,32 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
     }
 }
 
-template <int DT, int W, int CPL, bool GELU, bool SO>
+template <int DT, int W, int CPL, int RPW, bool GELU, bool SO>
 static void launch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, int recip,
                        hipStream_t stream) {
-    const int64_t rows = 4 / W;
+    const int64_t rows = (4 / W) * RPW;
     const dim3 grid(static_cast<unsigned>((M + rows - 1) / rows));
-    hipLaunchKernelGGL((quant_rows_vec<DT, W, CPL, GELU, SO>), grid, dim3(256), 0, stream, x, q,
+    hipLaunchKernelGGL((quant_rows_vec<DT, W, CPL, RPW, GELU, SO>), grid, dim3(256), 0, stream, x, q,
                        xs, M, K, recip);
 }
 
+// Rows of up to 128 chunks take one wave each; longer rows four waves, which
+// keeps more waves streaming per row (K = 3072 bf16: 23.5 us with 4 waves of 2
+// chunks per lane against 26.1 us with one wave of 6; a plain copy of the same
+// bytes takes 21.8 us).
 template <int DT, bool GELU, bool SO>
 static bool dispatch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, int recip,
                          hipStream_t stream) {
     constexpr int E = 16 / DType<DT>::bytes;
     const int64_t nchunks = K / E;
-    if (nchunks <= 64) launch_vec<DT, 1, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
-    else if (nchunks <= 128) launch_vec<DT, 1, 2, GELU, SO>(x, q, xs, M, K, recip, stream);
-    else if (nchunks <= 256) launch_vec<DT, 1, 4, GELU, SO>(x, q, xs, M, K, recip, stream);
-    else if (nchunks <= 384) launch_vec<DT, 1, 6, GELU, SO>(x, q, xs, M, K, recip, stream);
-    else if (nchunks <= 512) launch_vec<DT, 1, 8, GELU, SO>(x, q, xs, M, K, recip, stream);
-    else if (nchunks <= 1024) launch_vec<DT, 4, 4, GELU, SO>(x, q, xs, M, K, recip, stream);
-    else if (nchunks <= 1536) launch_vec<DT, 4, 6, GELU, SO>(x, q, xs, M, K, recip, stream);
-    else if (nchunks <= 2048) launch_vec<DT, 4, 8, GELU, SO>(x, q, xs, M, K, recip, stream);
+    if (nchunks <= 64) launch_vec<DT, 1, 1, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 128) launch_vec<DT, 1, 2, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 256) launch_vec<DT, 4, 1, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 512) launch_vec<DT, 4, 2, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 768) launch_vec<DT, 4, 3, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 1024) launch_vec<DT, 4, 4, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 1536) launch_vec<DT, 4, 6, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 2048) launch_vec<DT, 4, 8, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else return false;
     return true;
 }
