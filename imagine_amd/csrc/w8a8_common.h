@@ -118,6 +118,29 @@ __device__ __forceinline__ float gelu_tanh(float x) {
     return 0.5f * x * (1.0f + tanh_fast(inner));
 }
 
+// GELU-tanh of an epilogue output (rounded to a 16-bit output afterwards,
+// where one ulp of slack is allowed), in the reference's structure
+// 0.5 x (1 + tanh(u)) but with fewer operations than gelu_tanh:
+//   u = x (beta + beta kappa x^2)           (one fma; the reference's order
+//                                            rounds u differently by ~1 ulp)
+//   t = exp(-2|u|),  r = 1 - 2t / (1 + t)   (|tanh u|; the subtraction rounds
+//                                            like the reference's fp32 tanh, so
+//                                            1 + tanh(u) cancels as it does:
+//                                            exactly 0 once |u| > 9)
+//   gelu = (0.5 x) (1 + copysign(r, u))
+// Near u = 0 r carries an absolute error of ~2^-24, which only moves the
+// 1 + tanh(u) term by an ulp.  The quantizer's input activation, whose int8
+// codes are compared bit for bit, keeps gelu_tanh.
+__device__ __forceinline__ float gelu_tanh_fast(float x) {
+    const float kBeta = 0.79788456080286535588f;        // sqrt(2/pi)
+    const float kBetaKappa = 0.035677408136300125f;      // sqrt(2/pi) * 0.044715
+    const float kMinus2Log2e = -2.88539008177792681472f; // -2 / ln(2)
+    const float u = x * fmaf(kBetaKappa, x * x, kBeta);
+    const float t = __builtin_amdgcn_exp2f(fabsf(u) * kMinus2Log2e);   // (0, 1]
+    const float r = 1.0f - (t + t) * __builtin_amdgcn_rcpf(1.0f + t);
+    return (0.5f * x) * (1.0f + __builtin_copysignf(r, u));
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
 // where an index selects a register array element (MFMA accumulators), so the
 // array can never be indexed dynamically (which would demote it to scratch).
@@ -224,7 +247,7 @@ template <int ODT>
 __device__ __forceinline__ float epilogue_value(int acc, float xs, float ws, float bias, bool gelu) {
     float t = static_cast<float>(acc) * xs;
     float v = fmaf(t, ws, bias);
-    if (gelu) v = gelu_tanh(DType<ODT>::round(v));
+    if (gelu) v = gelu_tanh_fast(DType<ODT>::round(v));
     return v;
 }
 

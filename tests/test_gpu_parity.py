@@ -297,6 +297,47 @@ def test_dequantize_linear_bit_exact():
     assert np.array_equal(storage(out, "f16"), want)
 
 
+def _gelu_close(got, want, odt):
+    """The GELU epilogue's bar: one output ulp plus an absolute 2^-22, and at
+    least 99.9% of 16-bit outputs bit-equal to the oracle's."""
+    a = O.to_f32(got, odt).astype(np.float64)
+    b = O.to_f32(want, odt).astype(np.float64)
+    rel = {"bf16": 2.0**-7, "f16": 2.0**-10, "f32": 2.0**-18}[odt]
+    bad = np.abs(a - b) > np.abs(b) * rel + 2.0**-22
+    assert not bad.any(), f"{int(bad.sum())} outputs off by more than one ulp"
+    if odt != "f32":
+        assert (got == want).mean() > 0.999
+
+
+@pytest.mark.parametrize("odt", ["bf16", "f16"])
+def test_gemv_gelu_epilogue_within_one_ulp(odt):
+    m, n, k = 2, 4096, 3072
+    x = make_x(m, k, "bf16", seed=21)
+    q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    w = make_w(n, k, seed=22)
+    ws = torch.full((n,), 0.003)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(23)) * 0.5).to(TD[odt])
+    out = W.gemv_dequant(torch.from_numpy(q_ref).to(DEV), w.to(DEV), torch.from_numpy(xs_ref).to(DEV),
+                         ws.to(DEV), bias.to(DEV), TD[odt], gelu=True)
+    want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt),
+                              odt, act=1)
+    _gelu_close(storage(out, odt), want, odt)
+
+
+def test_dequantize_linear_gelu_within_one_ulp():
+    """Dequant + GELU over a wide range of pre-activations, the saturated
+    negative tail included (values down to about -12)."""
+    m, n = 64, 512
+    g = torch.Generator().manual_seed(5)
+    acc = torch.randint(-2**22, 2**22, (m, n), generator=g, dtype=torch.int32)
+    xs = torch.rand(m, generator=g) * 1e-3
+    ws = torch.rand(n, generator=g) * 3e-3
+    bias = (torch.randn(n, generator=g) * 0.5).to(torch.bfloat16)
+    out = W.dequantize_linear(acc.to(DEV), xs.to(DEV), ws.to(DEV), bias.to(DEV), torch.bfloat16, gelu=True)
+    want = O.epilogue_kitchen(acc.numpy(), xs.numpy(), ws.numpy(), storage(bias, "bf16"), "bf16", act=1)
+    _gelu_close(storage(out, "bf16"), want, "bf16")
+
+
 # ---------------------------------------------------------------- operator vs reference payloads
 
 
