@@ -14,11 +14,13 @@ namespace w8a8 {
 void launch_quantize(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M, int64_t K,
                      bool recip, bool gelu, bool scales_only, hipStream_t stream);
 void launch_gemv(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                 int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
-                 int64_t K, bool gelu, hipStream_t stream);
+                 int64_t ws_size, const void* bias, const Residual* res, void* out, int out_dtype,
+                 int64_t M, int64_t N, int64_t K, bool gelu, hipStream_t stream);
 void launch_gemm(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                 int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
-                 int64_t K, bool gelu, bool int32_out, hipStream_t stream);
+                 int64_t ws_size, const void* bias, const Residual* res, void* out, int out_dtype,
+                 int64_t M, int64_t N, int64_t K, bool gelu, bool int32_out, hipStream_t stream);
+void launch_residual(void* out, const void* resid, const void* rscale, int64_t rs_size, int dtype,
+                     int64_t M, int64_t N, hipStream_t stream);
 bool launch_gemm_xq(const void* x, int x_dtype, const float* xs, const int8_t* w, const float* ws,
                     int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M,
                     int64_t N, int64_t K, bool gelu, hipStream_t stream);
@@ -62,6 +64,14 @@ int check_ws(int64_t ws_size, int64_t N, const char* msg) {
     return W8A8_OK;
 }
 
+// Residual operands of the fused residual epilogue (cuda_linear.rs:707-744).
+int check_residual(const void* rscale, int64_t rscale_size, const void* resid, int64_t N) {
+    if (!rscale || !resid) return fail(W8A8_ERR_VALUE, "residual requires residual_scale");
+    if (rscale_size != 1 && rscale_size != N)
+        return fail(W8A8_ERR_RUNTIME, "residual_scale must be scalar or per-output-channel");
+    return W8A8_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -102,8 +112,26 @@ int w8a8_gemv_dequant(const int8_t* q, const int8_t* w, const float* xs, const f
     if (int rc = check_ws(ws_size, N, "INT8 GEMV weight scale must be scalar or per-output-channel")) return rc;
     if (N == 0) return W8A8_OK;
     if (!out || !xs || !ws || (K > 0 && (!q || !w))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
-    w8a8::launch_gemv(q, w, xs, ws, ws_size, bias, out, out_dtype, M, N, K,
+    w8a8::launch_gemv(q, w, xs, ws, ws_size, bias, nullptr, out, out_dtype, M, N, K,
                       flags & W8A8_ACT_GELU_TANH, stream);
+    return check_launch("int8_gemv_dequant");
+}
+
+int w8a8_gemv_dequant_residual(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                               int64_t ws_size, const void* bias, const void* rscale,
+                               int64_t rscale_size, const void* resid, void* out, int out_dtype,
+                               int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream) {
+    if (int rc = check_common(M, N, K, flags)) return rc;
+    if (flags & (W8A8_ACT_GELU_TANH | W8A8_OUT_INT32))
+        return fail(W8A8_ERR_VALUE, "the residual epilogue takes no output activation");
+    if (M != 1 && M != 2) return fail(W8A8_ERR_RUNTIME, "INT8 GEMV dequant expects M == 1 or M == 2");
+    if (!valid_dtype(out_dtype)) return fail(W8A8_ERR_RUNTIME, "Invalid INT8 GEMV output dtype code");
+    if (int rc = check_ws(ws_size, N, "INT8 GEMV weight scale must be scalar or per-output-channel")) return rc;
+    if (int rc = check_residual(rscale, rscale_size, resid, N)) return rc;
+    if (N == 0) return W8A8_OK;
+    if (!out || !xs || !ws || (K > 0 && (!q || !w))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    const w8a8::Residual res{rscale, rscale_size, resid};
+    w8a8::launch_gemv(q, w, xs, ws, ws_size, bias, &res, out, out_dtype, M, N, K, false, stream);
     return check_launch("int8_gemv_dequant");
 }
 
@@ -118,9 +146,37 @@ int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const f
     }
     if (M == 0 || N == 0) return W8A8_OK;
     if (!out || (K > 0 && (!q || !w)) || (!i32 && (!xs || !ws))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
-    w8a8::launch_gemm(q, w, xs, ws, ws_size, bias, out, i32 ? W8A8_F32 : out_dtype, M, N, K,
+    w8a8::launch_gemm(q, w, xs, ws, ws_size, bias, nullptr, out, i32 ? W8A8_F32 : out_dtype, M, N, K,
                       flags & W8A8_ACT_GELU_TANH, i32, stream);
     return check_launch("int8_gemm_dequant");
+}
+
+int w8a8_gemm_dequant_residual(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                               int64_t ws_size, const void* bias, const void* rscale,
+                               int64_t rscale_size, const void* resid, void* out, int out_dtype,
+                               int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream) {
+    if (int rc = check_common(M, N, K, flags)) return rc;
+    if (flags & (W8A8_ACT_GELU_TANH | W8A8_OUT_INT32))
+        return fail(W8A8_ERR_VALUE, "the residual epilogue takes no output activation");
+    if (!valid_dtype(out_dtype)) return fail(W8A8_ERR_RUNTIME, "Invalid INT8 linear output dtype code");
+    if (int rc = check_ws(ws_size, N, "INT8 weight scale must be scalar or per-output-channel")) return rc;
+    if (int rc = check_residual(rscale, rscale_size, resid, N)) return rc;
+    if (M == 0 || N == 0) return W8A8_OK;
+    if (!out || !xs || !ws || (K > 0 && (!q || !w))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    const w8a8::Residual res{rscale, rscale_size, resid};
+    w8a8::launch_gemm(q, w, xs, ws, ws_size, bias, &res, out, out_dtype, M, N, K, false, false, stream);
+    return check_launch("cutlass_int8_dequant_residual");
+}
+
+int w8a8_residual_apply(void* out, const void* resid, const void* rscale, int64_t rscale_size, int dtype,
+                        int64_t M, int64_t N, hipStream_t stream) {
+    if (M < 0 || N < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (!valid_dtype(dtype)) return fail(W8A8_ERR_RUNTIME, "Invalid output dtype code");
+    if (int rc = check_residual(rscale, rscale_size, resid, N)) return rc;
+    if (M == 0 || N == 0) return W8A8_OK;
+    if (!out) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    w8a8::launch_residual(out, resid, rscale, rscale_size, dtype, M, N, stream);
+    return check_launch("apply_residual");
 }
 
 int w8a8_gemm_dequant_xq(const void* x, int x_dtype, const float* xs, const int8_t* w,
@@ -160,9 +216,18 @@ int64_t w8a8_int8_linear_workspace_bytes(int64_t M, int64_t K) {
     return (M * K + 255) / 256 * 256 + M * 4;
 }
 
-int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
-                     const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
-                     uint32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The operator's route policy, shared by the entries with and without a
+// residual (res == nullptr: none).  The residual is fused into the GEMM or
+// GEMV epilogue; the reference fuses it on its CUTLASS and M = 1 routes and
+// applies it eagerly elsewhere, with the same single fma either way.
+int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
+                     const void* bias, const w8a8::Residual* res, void* out, int out_dtype, int64_t M,
+                     int64_t N, int64_t K, uint32_t flags, void* workspace, int64_t workspace_bytes,
+                     hipStream_t stream) {
     if (int rc = check_common(M, N, K, flags)) return rc;
     if (flags & W8A8_OUT_INT32) return fail(W8A8_ERR_VALUE, "W8A8_OUT_INT32 is a GEMM-only flag");
     if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
@@ -171,6 +236,9 @@ int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* w
     if (int rc = check_ws(ws_size, N, gemv ? "INT8 GEMV weight scale must be scalar or per-output-channel"
                                            : "INT8 weight scale must be scalar or per-output-channel"))
         return rc;
+    if (res) {
+        if (int rc = check_residual(res->rscale, res->rs_size, res->resid, N)) return rc;
+    }
     if (!gemv && K % 4 != 0 && M > 0 && N > 0)
         return fail(W8A8_ERR_RUNTIME,
                     "INT8 GEMM not supported on this GPU for these dimensions (requires SM >= 7.5, "
@@ -187,18 +255,50 @@ int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* w
     // The input activation is applied before quantization; the GEMM/GEMV
     // epilogue itself runs without GELU here.
     // Fused route: row scales, then a GEMM that quantizes its activation tiles
-    // (an input activation is only applied by the standalone quantizer).
+    // (an input activation is only applied by the standalone quantizer); a
+    // residual is then applied by the standalone residual kernel.
     if (!gemv && (flags & W8A8_FUSED_QUANT) && !(qflags & W8A8_ACT_GELU_TANH) && N > 0 &&
         x_dtype != W8A8_F32 && K % 16 == 0) {
         if (int rc = w8a8_row_scales(x, x_dtype, xs, M, K, qflags, stream)) return rc;
         if (w8a8::launch_gemm_xq(x, x_dtype, xs, w, ws, ws_size, bias, out, out_dtype, M, N, K,
-                                 false, stream))
-            return check_launch("int8_gemm_dequant_xq");
+                                 false, stream)) {
+            if (int rc = check_launch("int8_gemm_dequant_xq")) return rc;
+            if (!res) return W8A8_OK;
+            return w8a8_residual_apply(out, res->resid, res->rscale, res->rs_size, out_dtype, M, N, stream);
+        }
     }
     if (int rc = w8a8_quantize_rowwise(x, x_dtype, q, xs, M, K, qflags, stream)) return rc;
     if (N == 0) return W8A8_OK;
+    if (res) {
+        if (gemv)
+            return w8a8_gemv_dequant_residual(q, w, xs, ws, ws_size, bias, res->rscale, res->rs_size,
+                                              res->resid, out, out_dtype, M, N, K, 0, stream);
+        return w8a8_gemm_dequant_residual(q, w, xs, ws, ws_size, bias, res->rscale, res->rs_size,
+                                          res->resid, out, out_dtype, M, N, K, 0, stream);
+    }
     if (gemv) return w8a8_gemv_dequant(q, w, xs, ws, ws_size, bias, out, out_dtype, M, N, K, 0, stream);
     return w8a8_gemm_dequant(q, w, xs, ws, ws_size, bias, out, out_dtype, M, N, K, 0, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
+                     const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                     uint32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, nullptr, out, out_dtype, M, N, K, flags,
+                            workspace, workspace_bytes, stream);
+}
+
+int w8a8_int8_linear_residual(const void* x, int x_dtype, const int8_t* w, const float* ws,
+                              int64_t ws_size, const void* bias, const void* rscale,
+                              int64_t rscale_size, const void* resid, void* out, int out_dtype,
+                              int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
+                              int64_t workspace_bytes, hipStream_t stream) {
+    const w8a8::Residual res{rscale, rscale_size, resid};
+    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, &res, out, out_dtype, M, N, K, flags,
+                            workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

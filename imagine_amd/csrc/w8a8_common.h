@@ -251,6 +251,25 @@ __device__ __forceinline__ float epilogue_value(int acc, float xs, float ws, flo
     return v;
 }
 
+// Residual of the pre-norm block fused into an epilogue:
+//   out = O( fma(O(lin), rscale[n], resid[m, n]) )
+// with rscale (1 or N entries) and resid ([M, N]) in the output dtype: the
+// reference's fused CUTLASS residual (archived cutlass_gemm_int8.cu:122-188)
+// and, bit for bit, its eager addcmul on the GPU (int8_linear.rs:99-111).
+struct Residual {
+    const void* rscale;
+    int64_t rs_size;
+    const void* resid;
+};
+
+template <int ODT>
+__device__ __forceinline__ float residual_value(float lin, const Residual& res, int64_t m, int n, int N) {
+    using OS = typename DType<ODT>::storage;
+    const float s = DType<ODT>::load(static_cast<const OS*>(res.rscale)[res.rs_size == 1 ? 0 : n]);
+    const float r = DType<ODT>::load(static_cast<const OS*>(res.resid)[m * N + n]);
+    return fmaf(DType<ODT>::round(lin), s, r);
+}
+
 // ---------------------------------------------------------------- wave reductions
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -12,13 +12,15 @@ namespace w8a8 {
 constexpr int kBN = 256, kBM = 256, kBK = 64, kWN = 128, kWM = 128;
 constexpr int kGroupM = 4;
 
+constexpr Residual kNoResidual{nullptr, 0, nullptr};
+
 template <int ODT, int MODE, bool GELU, int XDT>
 static void launch_mfma(const int8_t* q, const void* x, const int8_t* w, const float* xs,
-                        const float* ws, int64_t ws_size, const void* bias, void* out, int64_t M,
-                        int64_t N, int64_t K, hipStream_t stream) {
+                        const float* ws, int64_t ws_size, const void* bias, const Residual& res,
+                        void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
     const int tiles = static_cast<int>(((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN));
     hipLaunchKernelGGL((gemm_mfma<ODT, MODE, GELU, XDT, kBN, kBM, kBK, kWN, kWM>), dim3(tiles),
-                       dim3(256), 0, stream, q, x, w, xs, ws, ws_size, bias, out,
+                       dim3(256), 0, stream, q, x, w, xs, ws, ws_size, bias, res, out,
                        static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), kGroupM);
 }
 
@@ -74,76 +76,72 @@ static bool buffer_loads_disabled() {
 
 template <int ODT, int MODE, bool GELU, class C>
 static void launch_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                       int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
-                       hipStream_t stream) {
+                       int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
+                       int64_t N, int64_t K, hipStream_t stream) {
     const int tiles = static_cast<int>(((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN));
     // buffer-resource loads take 32-bit offsets: both operands below 2 GiB
     const int64_t kBufLimit = (1ll << 31) - 4096;
     if (M * K < kBufLimit && N * K < kBufLimit && !buffer_loads_disabled())
         hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C, true>), dim3(tiles), dim3(C::kThreads), 0, stream,
-                           q, w, xs, ws, ws_size, bias, out, static_cast<int>(M), static_cast<int>(N),
+                           q, w, xs, ws, ws_size, bias, res, out, static_cast<int>(M), static_cast<int>(N),
                            static_cast<int>(K), kGroupM);
     else
         hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C, false>), dim3(tiles), dim3(C::kThreads), 0, stream,
-                           q, w, xs, ws, ws_size, bias, out, static_cast<int>(M), static_cast<int>(N),
+                           q, w, xs, ws, ws_size, bias, res, out, static_cast<int>(M), static_cast<int>(N),
                            static_cast<int>(K), kGroupM);
 }
 
 template <int ODT, int MODE, bool GELU>
 static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                    int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N, int64_t K,
-                    hipStream_t stream) {
+                    int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
+                    int64_t N, int64_t K, hipStream_t stream) {
     const int choice = mainloop_choice();
     // whole K tiles only (the DMA ring has no tail masking)
     if (choice == 0) return false;
     if (choice == 5 && K % CfgN256M192W8::BK == 0) {
-        launch_dma<ODT, MODE, GELU, CfgN256M192W8>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+        launch_dma<ODT, MODE, GELU, CfgN256M192W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
         return true;
     }
     if (choice == 4 && K % CfgN256M256W8::BK == 0) {
-        launch_dma<ODT, MODE, GELU, CfgN256M256W8>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+        launch_dma<ODT, MODE, GELU, CfgN256M256W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
         return true;
     }
     if (choice == 3 && K % CfgN256M256::BK == 0) {
-        launch_dma<ODT, MODE, GELU, CfgN256M256>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+        launch_dma<ODT, MODE, GELU, CfgN256M256>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
         return true;
     }
     if (K % CfgN256M128::BK != 0) return false;
-    launch_dma<ODT, MODE, GELU, CfgN256M128>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream);
+    launch_dma<ODT, MODE, GELU, CfgN256M128>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
     return true;
 }
 
-template <int ODT, bool GELU>
-static void gemm_dispatch_odt(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                              int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N,
-                              int64_t K, bool int32_out, hipStream_t stream) {
+// One output mode of one output dtype: the DMA main loop where it applies, the
+// register-staged main loop for other K % 16 == 0 shapes, else the generic kernel.
+template <int ODT, int MODE, bool GELU>
+static void gemm_dispatch(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                          int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
+                          int64_t N, int64_t K, hipStream_t stream) {
     const bool fast = gemm_mfma_supported(q, 1, w, M, N, K);
-    if constexpr (ODT == W8A8_F32 && !GELU) {   // the int32 mode is instantiated once
-        if (int32_out) {
-            if (fast && try_dma<ODT, 1, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream)) return;
-            if (fast) launch_mfma<ODT, 1, false, -1>(q, nullptr, w, xs, ws, ws_size, bias, out, M, N, K, stream);
-            else hipLaunchKernelGGL((gemm_generic<ODT, 1, false>), dim3(static_cast<unsigned>((M * N + 255) / 256)),
-                                    dim3(256), 0, stream, q, w, xs, ws, ws_size, bias, out, M, N, K);
-            return;
-        }
-    }
-    if (fast && try_dma<ODT, 0, GELU>(q, w, xs, ws, ws_size, bias, out, M, N, K, stream)) return;
-    if (fast) launch_mfma<ODT, 0, GELU, -1>(q, nullptr, w, xs, ws, ws_size, bias, out, M, N, K, stream);
-    else hipLaunchKernelGGL((gemm_generic<ODT, 0, GELU>), dim3(static_cast<unsigned>((M * N + 255) / 256)),
-                            dim3(256), 0, stream, q, w, xs, ws, ws_size, bias, out, M, N, K);
+    if (fast && try_dma<ODT, MODE, GELU>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream)) return;
+    if (fast) launch_mfma<ODT, MODE, GELU, -1>(q, nullptr, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
+    else hipLaunchKernelGGL((gemm_generic<ODT, MODE, GELU>), dim3(static_cast<unsigned>((M * N + 255) / 256)),
+                            dim3(256), 0, stream, q, w, xs, ws, ws_size, bias, res, out, M, N, K);
 }
 
+// res == nullptr: no residual.  The int32 mode is instantiated once (f32
+// storage type), the residual mode without GELU.
 void launch_gemm(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                 int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
-                 int64_t K, bool gelu, bool int32_out, hipStream_t stream) {
+                 int64_t ws_size, const void* bias, const Residual* res, void* out, int out_dtype,
+                 int64_t M, int64_t N, int64_t K, bool gelu, bool int32_out, hipStream_t stream) {
     if (int32_out) {
-        gemm_dispatch_odt<W8A8_F32, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, true, stream);
+        gemm_dispatch<W8A8_F32, 1, false>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, stream);
         return;
     }
 #define W8A8_GEMM_CASE(ODT)                                                                       \
     if (out_dtype == ODT) {                                                                       \
-        if (gelu) gemm_dispatch_odt<ODT, true>(q, w, xs, ws, ws_size, bias, out, M, N, K, false, stream); \
-        else gemm_dispatch_odt<ODT, false>(q, w, xs, ws, ws_size, bias, out, M, N, K, false, stream); \
+        if (res) gemm_dispatch<ODT, 2, false>(q, w, xs, ws, ws_size, bias, *res, out, M, N, K, stream); \
+        else if (gelu) gemm_dispatch<ODT, 0, true>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, stream); \
+        else gemm_dispatch<ODT, 0, false>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, stream); \
         return;                                                                                   \
     }
     W8A8_GEMM_CASE(W8A8_BF16)
@@ -160,8 +158,8 @@ bool launch_gemm_xq(const void* x, int x_dtype, const float* xs, const int8_t* w
     if (!gemm_mfma_supported(x, 2, w, M, N, K)) return false;
 #define W8A8_XQ_CASE(ODT, XDT)                                                                    \
     if (out_dtype == ODT && x_dtype == XDT) {                                                     \
-        if (gelu) launch_mfma<ODT, 0, true, XDT>(nullptr, x, w, xs, ws, ws_size, bias, out, M, N, K, stream); \
-        else launch_mfma<ODT, 0, false, XDT>(nullptr, x, w, xs, ws, ws_size, bias, out, M, N, K, stream); \
+        if (gelu) launch_mfma<ODT, 0, true, XDT>(nullptr, x, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, stream); \
+        else launch_mfma<ODT, 0, false, XDT>(nullptr, x, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, stream); \
         return true;                                                                              \
     }
     W8A8_XQ_CASE(W8A8_BF16, W8A8_BF16)
@@ -188,6 +186,39 @@ void launch_dequant(const int32_t* acc, const float* xs, const float* ws, int64_
     W8A8_DQ_CASE(W8A8_F16)
     W8A8_DQ_CASE(W8A8_F32)
 #undef W8A8_DQ_CASE
+}
+
+// Standalone residual step over an existing output: out = O(fma(out, rscale, resid)).
+// The reference's eager apply_residual (inference/src/int8_linear.rs:99-111),
+// for routes whose epilogue did not fuse it.
+template <int ODT>
+__global__ __launch_bounds__(256) void residual_apply(void* __restrict__ out, const void* __restrict__ resid,
+                                                      const void* __restrict__ rscale, int64_t rs_size,
+                                                      int64_t M, int64_t N) {
+    using OS = typename DType<ODT>::storage;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= M * N) return;
+    const int64_t n = idx % N;
+    OS* o = static_cast<OS*>(out);
+    const float s = DType<ODT>::load(static_cast<const OS*>(rscale)[rs_size == 1 ? 0 : n]);
+    const float r = DType<ODT>::load(static_cast<const OS*>(resid)[idx]);
+    o[idx] = DType<ODT>::store(fmaf(DType<ODT>::load(o[idx]), s, r));
+}
+
+void launch_residual(void* out, const void* resid, const void* rscale, int64_t rs_size, int dtype,
+                     int64_t M, int64_t N, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((M * N + 255) / 256));
+    switch (dtype) {
+        case W8A8_BF16:
+            hipLaunchKernelGGL((residual_apply<W8A8_BF16>), grid, dim3(256), 0, stream, out, resid, rscale, rs_size, M, N);
+            break;
+        case W8A8_F16:
+            hipLaunchKernelGGL((residual_apply<W8A8_F16>), grid, dim3(256), 0, stream, out, resid, rscale, rs_size, M, N);
+            break;
+        default:
+            hipLaunchKernelGGL((residual_apply<W8A8_F32>), grid, dim3(256), 0, stream, out, resid, rscale, rs_size, M, N);
+            break;
+    }
 }
 
 }  // namespace w8a8

@@ -59,16 +59,18 @@ __device__ __forceinline__ TileCoord tile_of_block(int bid, int tiles_m, int til
 // m = m_base + wave_m + 32 j + lane % 32 and channels
 // n = n_base + wave_n + 32 i + 8 g + 4 (lane / 32) + {0,1,2,3} in acc[i][j][4g .. 4g+3].
 // All accumulator indices are compile-time constants (static_for).
+// MODE: 0 = output dtype, 1 = int32 accumulators, 2 = output dtype + residual.
 template <int ODT, int MODE, bool GELU, int TN, int TM>
 __device__ __forceinline__ void store_tiles(const v16i (&acc)[TN][TM], int lane, int m_base,
                                             int n_base, int wave_m, int wave_n, int M, int N,
                                             const float* __restrict__ xs,
                                             const float* __restrict__ ws, int64_t ws_size,
-                                            const void* __restrict__ bias, void* __restrict__ out) {
+                                            const void* __restrict__ bias, const Residual& res,
+                                            void* __restrict__ out) {
     const int lane_m = lane % 32;
     const int lane_n = 4 * (lane / 32);
     float xsv[TM];
-    if constexpr (MODE == 0) {
+    if constexpr (MODE != 1) {
         static_for<0, TM>([&](auto j) {
             const int m = m_base + wave_m + j * 32 + lane_m;
             xsv[j] = xs[m < M ? m : M - 1];
@@ -79,7 +81,7 @@ __device__ __forceinline__ void store_tiles(const v16i (&acc)[TN][TM], int lane,
         static_for<0, 4>([&](auto g) {
             const int n0 = n_base + wave_n + i * 32 + 8 * g + lane_n;
             float wsv[4], bv[4];
-            if constexpr (MODE == 0) {
+            if constexpr (MODE != 1) {
                 static_for<0, 4>([&](auto e) {
                     const int n = n0 + e < N ? n0 + e : N - 1;
                     wsv[e] = ws[ws_size == 1 ? 0 : n];
@@ -107,6 +109,10 @@ __device__ __forceinline__ void store_tiles(const v16i (&acc)[TN][TM], int lane,
                         float v[4];
                         static_for<0, 4>([&](auto e) {
                             v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
+                            if constexpr (MODE == 2) {
+                                const int n = n0 + e < N ? n0 + e : N - 1;
+                                v[e] = residual_value<ODT>(v[e], res, m, n, N);
+                            }
                         });
                         using OS = typename DType<ODT>::storage;
                         OS* o = static_cast<OS*>(out) + row;
@@ -149,7 +155,8 @@ template <int ODT, int MODE, bool GELU, int XDT, int BN, int BM, int BK, int WN,
 __global__ __launch_bounds__(256, 1) void gemm_mfma(
     const int8_t* __restrict__ q, const void* __restrict__ xsrc, const int8_t* __restrict__ w,
     const float* __restrict__ xs, const float* __restrict__ ws, int64_t ws_size,
-    const void* __restrict__ bias, void* __restrict__ out, int M, int N, int K, int group_m) {
+    const void* __restrict__ bias, Residual res, void* __restrict__ out, int M, int N, int K,
+    int group_m) {
     using S = GemmShape<BN, BM, BK, WN, WM>;
     constexpr bool XQ = XDT >= 0;          // activation quantized in the tile load
     constexpr int XDTq = XQ ? XDT : W8A8_BF16;
@@ -289,7 +296,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma(
     }
 
     store_tiles<ODT, MODE, GELU, S::TN, S::TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
-                                               ws_size, bias, out);
+                                               ws_size, bias, res, out);
 }
 
 // ---------------------------------------------------------------- LDS-DMA main loop
@@ -379,9 +386,13 @@ struct DmaCfg {
     static constexpr int CPR = BK / 16;                    // 16-byte chunks per LDS row
     static constexpr int KS = BK / 32;                     // k32 substeps per tile
     static constexpr int kTileBytes = (BN + BM) * BK;      // one stage: weights then activations
+    static_assert(kTileBytes % 1024 == 0, "whole 1 KB wave-loads per stage");
     static constexpr int kWaveLoads = kTileBytes / 1024;   // 1 KB per wave-load
-    static_assert(kWaveLoads % kWaves == 0, "wave-loads split evenly over the waves");
-    static constexpr int kLoadsPerThread = kWaveLoads / kWaves;
+    // Wave-load L = j * kWaves + wave: the first kWaveLoads % kWaves waves
+    // issue one more per tile than the others when the split is uneven.
+    static constexpr int kLoadsPerThread = (kWaveLoads + kWaves - 1) / kWaves;
+    static constexpr int kLoadsFew = kWaveLoads / kWaves;
+    static constexpr int kWavesWithMore = kWaveLoads % kWaves;
     static constexpr int kWWaveLoads = BN * BK / 1024;
     static_assert(kLoadsPerThread * (STAGES - 2) < 64, "vmcnt range");
     static_assert(BK == 64 || BK == 96 || BK == 128, "K tile of 64, 96 or 128 bytes");
@@ -400,13 +411,16 @@ __device__ __forceinline__ int out_swz(int row) {
 // Dequantize the block's accumulators into the LDS ring as a BM x BN tile of
 // 16-bit values, then write it out row by row, 16 bytes per lane (N % 8 == 0,
 // 16-byte aligned out).  Same values as store_tiles.
-template <int ODT, bool GELU, class C>
+// MODE 2 adds the residual in the write-out pass, where the residual row and
+// the scales are read as 16-byte chunks (resid and a per-channel rscale
+// 16-byte aligned, which the caller checks).
+template <int ODT, int MODE, bool GELU, class C>
 __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::TM], int8_t* lds,
                                                    int lane, int t, int m_base, int n_base,
                                                    int wave_m, int wave_n, int M, int N,
                                                    const float* __restrict__ xs,
                                                    const float* __restrict__ ws, int64_t ws_size,
-                                                   const void* __restrict__ bias,
+                                                   const void* __restrict__ bias, const Residual& res,
                                                    void* __restrict__ out) {
     constexpr int BN = C::BN, BM = C::BM, TN = C::TN, TM = C::TM;
     constexpr int kRowBytes = BN * 2;
@@ -450,15 +464,37 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
         const int idx = pass * C::kThreads + t;
         const int r = idx / kChunks, c = idx % kChunks;
         const int m = m_base + r, n = n_base + c * 8;
-        const uint4 v = *reinterpret_cast<const uint4*>(lds + r * kRowBytes + (c ^ out_swz<BN>(r)) * 16);
-        if (m < M && n < N) *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
+        uint4 v = *reinterpret_cast<const uint4*>(lds + r * kRowBytes + (c ^ out_swz<BN>(r)) * 16);
+        if (m < M && n < N) {
+            if constexpr (MODE == 2) {
+                const uint4 rv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.resid) +
+                                                                 static_cast<int64_t>(m) * N + n);
+                uint4 sv;
+                if (res.rs_size == 1) {
+                    const uint32_t s1 = static_cast<const OS*>(res.rscale)[0];
+                    sv.x = sv.y = sv.z = sv.w = s1 | (s1 << 16);
+                } else {
+                    sv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.rscale) + n);
+                }
+                auto lo = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w & 0xffffu)); };
+                auto hi = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w >> 16)); };
+                auto fuse = [&](uint32_t lin, uint32_t s, uint32_t rr) {
+                    return DType<ODT>::store2(fmaf(lo(lin), lo(s), lo(rr)), fmaf(hi(lin), hi(s), hi(rr)));
+                };
+                v.x = fuse(v.x, sv.x, rv.x);
+                v.y = fuse(v.y, sv.y, rv.y);
+                v.z = fuse(v.z, sv.z, rv.z);
+                v.w = fuse(v.w, sv.w, rv.w);
+            }
+            *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
+        }
     }
 }
 
 template <int ODT, int MODE, bool GELU, class C, bool BUF>
 __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     const int8_t* __restrict__ q, const int8_t* __restrict__ w, const float* __restrict__ xs,
-    const float* __restrict__ ws, int64_t ws_size, const void* __restrict__ bias,
+    const float* __restrict__ ws, int64_t ws_size, const void* __restrict__ bias, Residual res,
     void* __restrict__ out, int M, int N, int K, int group_m) {
     constexpr int BN = C::BN, BM = C::BM, WN = C::WN, WM = C::WM, BK = C::BK, STAGES = C::STAGES;
     constexpr int TN = C::TN, TM = C::TM, CPR = C::CPR, KS = C::KS;
@@ -477,15 +513,15 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     const int KT = K / BK;                                 // K % BK == 0 (host checks)
 
     // Source of each wave-load this lane takes part in: wave-load L (global
-    // index wave * kLoadsPerThread + j) fills LDS chunks [64 L, 64 L + 64) of the
-    // stage; chunk p holds row p / CPR, logical chunk (p % CPR) ^ swz(row).
+    // index j * kWaves + wave, L < kWaveLoads) fills LDS chunks [64 L, 64 L + 64)
+    // of the stage; chunk p holds row p / CPR, logical chunk (p % CPR) ^ swz(row).
     // BUF: byte offsets into a buffer resource per operand (the K offset of a
     // tile goes in the scalar offset), else 64-bit global addresses.
     uint32_t voff[kLoadsPerThread];
     const int8_t* src[BUF ? 1 : kLoadsPerThread];
 #pragma unroll
     for (int j = 0; j < kLoadsPerThread; ++j) {
-        const int L = wave * kLoadsPerThread + j;
+        const int L = j * C::kWaves + wave < C::kWaveLoads ? j * C::kWaves + wave : C::kWaveLoads - 1;
         const bool is_w = L < kWWaveLoads;
         const int p = (is_w ? L : L - kWWaveLoads) * 64 + lane;
         const int r = p / CPR;
@@ -500,7 +536,8 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
         const int k0 = kt * BK;
 #pragma unroll
         for (int j = 0; j < kLoadsPerThread; ++j) {
-            const int L = wave * kLoadsPerThread + j;
+            const int L = j * C::kWaves + wave;
+            if (C::kWavesWithMore != 0 && L >= C::kWaveLoads) break;   // wave-uniform
             int8_t* dst = lds + stage * kTileBytes + L * 1024;
             if constexpr (BUF) {
                 buffer_load_lds16(L < kWWaveLoads ? static_cast<const void*>(w) : static_cast<const void*>(q), dst,
@@ -563,7 +600,10 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     auto wait_tile = [&](int after) {
         static_for<0, STAGES - 1>([&](auto a) {
             constexpr int A = decltype(a)::value;
-            if (after == A) wait_vm_lgkm0<A * kLoadsPerThread>();
+            if (after == A) {
+                if (C::kWavesWithMore == 0 || wave < C::kWavesWithMore) wait_vm_lgkm0<A * kLoadsPerThread>();
+                else wait_vm_lgkm0<A * C::kLoadsFew>();
+            }
         });
     };
 
@@ -625,16 +665,19 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
         if (kt < KT) tile(kt, stage, next_stage(stage), std::integral_constant<int, 0>{});
     }
 
-    if constexpr (MODE == 0 && ODT != W8A8_F32 && C::kStageOut) {
-        const bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+    if constexpr (MODE != 1 && ODT != W8A8_F32 && C::kStageOut) {
+        bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+        if constexpr (MODE == 2)
+            vec_ok = vec_ok && (reinterpret_cast<uintptr_t>(res.resid) % 16) == 0 &&
+                     (res.rs_size == 1 || (reinterpret_cast<uintptr_t>(res.rscale) % 16) == 0);
         if (vec_ok) {
-            store_tiles_staged<ODT, GELU, C>(acc, lds, lane, t, m_base, n_base, wave_m, wave_n, M, N,
-                                             xs, ws, ws_size, bias, out);
+            store_tiles_staged<ODT, MODE, GELU, C>(acc, lds, lane, t, m_base, n_base, wave_m, wave_n, M, N,
+                                                   xs, ws, ws_size, bias, res, out);
             return;
         }
     }
     store_tiles<ODT, MODE, GELU, TN, TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
-                                         ws_size, bias, out);
+                                         ws_size, bias, res, out);
 }
 
 // Generic GEMM for shapes the MFMA kernel does not take (K % 16 != 0,
@@ -644,7 +687,7 @@ __global__ __launch_bounds__(256) void gemm_generic(const int8_t* __restrict__ q
                                                     const int8_t* __restrict__ w,
                                                     const float* __restrict__ xs,
                                                     const float* __restrict__ ws, int64_t ws_size,
-                                                    const void* __restrict__ bias,
+                                                    const void* __restrict__ bias, Residual res,
                                                     void* __restrict__ out, int64_t M, int64_t N,
                                                     int64_t K) {
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -656,8 +699,9 @@ __global__ __launch_bounds__(256) void gemm_generic(const int8_t* __restrict__ q
         static_cast<int32_t*>(out)[idx] = acc;
     } else {
         const float b = bias ? DType<ODT>::load(static_cast<const typename DType<ODT>::storage*>(bias)[n]) : 0.0f;
-        static_cast<typename DType<ODT>::storage*>(out)[idx] =
-            DType<ODT>::store(epilogue_value<ODT>(acc, xs[m], ws[ws_size == 1 ? 0 : n], b, GELU));
+        float v = epilogue_value<ODT>(acc, xs[m], ws[ws_size == 1 ? 0 : n], b, GELU);
+        if constexpr (MODE == 2) v = residual_value<ODT>(v, res, m, static_cast<int>(n), static_cast<int>(N));
+        static_cast<typename DType<ODT>::storage*>(out)[idx] = DType<ODT>::store(v);
     }
 }
 

@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void gemv_vec(const int8_t* __restrict__ q,
                                                 const int8_t* __restrict__ w,
                                                 const float* __restrict__ xs,
                                                 const float* __restrict__ ws, int64_t ws_size,
-                                                const void* __restrict__ bias,
+                                                const void* __restrict__ bias, Residual res,
                                                 void* __restrict__ out, int64_t N, int64_t K,
                                                 int gelu) {
     const int lane = threadIdx.x % kWave;
@@ -113,9 +113,11 @@ __global__ __launch_bounds__(256) void gemv_vec(const int8_t* __restrict__ q,
                     const float wsn = ws[ws_size == 1 ? 0 : n];
                     const float b = bias ? load_bias<ODT>(bias, n) : 0.0f;
 #pragma unroll
-                    for (int m = 0; m < MR; ++m)
-                        store_out<ODT>(out, m * N + n,
-                                       epilogue_value<ODT>(acc[m][r], xsc[m], wsn, b, gelu != 0));
+                    for (int m = 0; m < MR; ++m) {
+                        float v = epilogue_value<ODT>(acc[m][r], xsc[m], wsn, b, gelu != 0);
+                        if (res.resid) v = residual_value<ODT>(v, res, m, static_cast<int>(n), static_cast<int>(N));
+                        store_out<ODT>(out, m * N + n, v);
+                    }
                 }
             }
         }
@@ -129,8 +131,8 @@ __global__ __launch_bounds__(256) void gemv_generic(const int8_t* __restrict__ q
                                                     const float* __restrict__ xs,
                                                     const float* __restrict__ ws,
                                                     int64_t ws_size, const void* __restrict__ bias,
-                                                    void* __restrict__ out, int64_t M, int64_t N,
-                                                    int64_t K, int gelu) {
+                                                    Residual res, void* __restrict__ out, int64_t M,
+                                                    int64_t N, int64_t K, int gelu) {
     const int lane = threadIdx.x % kWave;
     const int64_t n = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
     if (n >= N) return;
@@ -141,23 +143,24 @@ __global__ __launch_bounds__(256) void gemv_generic(const int8_t* __restrict__ q
         acc = wave_sum(acc);
         if (lane == 0) {
             const float b = bias ? load_bias<ODT>(bias, n) : 0.0f;
-            store_out<ODT>(out, m * N + n,
-                           epilogue_value<ODT>(acc, xs[m], ws[ws_size == 1 ? 0 : n], b, gelu != 0));
+            float v = epilogue_value<ODT>(acc, xs[m], ws[ws_size == 1 ? 0 : n], b, gelu != 0);
+            if (res.resid) v = residual_value<ODT>(v, res, m, static_cast<int>(n), static_cast<int>(N));
+            store_out<ODT>(out, m * N + n, v);
         }
     }
 }
 
 template <int ODT, int MR, int RPW, int XC>
 static void launch_gemv_vec(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                            int64_t ws_size, const void* bias, void* out, int64_t N, int64_t K,
+                            int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t N, int64_t K,
                             int gelu, int blocks, hipStream_t stream) {
     hipLaunchKernelGGL((gemv_vec<ODT, MR, RPW, XC>), dim3(blocks), dim3(256), 0, stream, q, w, xs,
-                       ws, ws_size, bias, out, N, K, gelu);
+                       ws, ws_size, bias, res, out, N, K, gelu);
 }
 
 template <int ODT, int MR>
 static void gemv_dispatch_m(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                            int64_t ws_size, const void* bias, void* out, int64_t N, int64_t K,
+                            int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t N, int64_t K,
                             int gelu, hipStream_t stream) {
     constexpr int RPW = 2;
     // Enough waves to keep every CU streaming, never more than one pass of channels.
@@ -166,38 +169,40 @@ static void gemv_dispatch_m(const int8_t* q, const int8_t* w, const float* xs, c
     if (blocks > 2048) blocks = 2048;
     const int64_t nchunks = K / 16;
     const int b = static_cast<int>(blocks);
-    if (nchunks <= 64) launch_gemv_vec<ODT, MR, RPW, 1>(q, w, xs, ws, ws_size, bias, out, N, K, gelu, b, stream);
-    else if (nchunks <= 128) launch_gemv_vec<ODT, MR, RPW, 2>(q, w, xs, ws, ws_size, bias, out, N, K, gelu, b, stream);
-    else if (nchunks <= 192) launch_gemv_vec<ODT, MR, RPW, 3>(q, w, xs, ws, ws_size, bias, out, N, K, gelu, b, stream);
-    else if (nchunks <= 256) launch_gemv_vec<ODT, MR, RPW, 4>(q, w, xs, ws, ws_size, bias, out, N, K, gelu, b, stream);
-    else if (nchunks <= 384) launch_gemv_vec<ODT, MR, RPW, 6>(q, w, xs, ws, ws_size, bias, out, N, K, gelu, b, stream);
-    else launch_gemv_vec<ODT, MR, RPW, 0>(q, w, xs, ws, ws_size, bias, out, N, K, gelu, b, stream);
+    if (nchunks <= 64) launch_gemv_vec<ODT, MR, RPW, 1>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, b, stream);
+    else if (nchunks <= 128) launch_gemv_vec<ODT, MR, RPW, 2>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, b, stream);
+    else if (nchunks <= 192) launch_gemv_vec<ODT, MR, RPW, 3>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, b, stream);
+    else if (nchunks <= 256) launch_gemv_vec<ODT, MR, RPW, 4>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, b, stream);
+    else if (nchunks <= 384) launch_gemv_vec<ODT, MR, RPW, 6>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, b, stream);
+    else launch_gemv_vec<ODT, MR, RPW, 0>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, b, stream);
 }
 
 template <int ODT>
 static void gemv_dispatch(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                          int64_t ws_size, const void* bias, void* out, int64_t M, int64_t N,
-                          int64_t K, int gelu, hipStream_t stream) {
+                          int64_t ws_size, const void* bias, const Residual& res, void* out,
+                          int64_t M, int64_t N, int64_t K, int gelu, hipStream_t stream) {
     const bool vec = K % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(w) % 16 == 0 && (M == 1 || M == 2);
     if (vec) {
-        if (M == 1) gemv_dispatch_m<ODT, 1>(q, w, xs, ws, ws_size, bias, out, N, K, gelu, stream);
-        else gemv_dispatch_m<ODT, 2>(q, w, xs, ws, ws_size, bias, out, N, K, gelu, stream);
+        if (M == 1) gemv_dispatch_m<ODT, 1>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, stream);
+        else gemv_dispatch_m<ODT, 2>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, stream);
         return;
     }
     const dim3 grid(static_cast<unsigned>((N + 3) / 4));
     hipLaunchKernelGGL((gemv_generic<ODT>), grid, dim3(256), 0, stream, q, w, xs, ws, ws_size, bias,
-                       out, M, N, K, gelu);
+                       res, out, M, N, K, gelu);
 }
 
+// res == nullptr: no residual.
 void launch_gemv(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                 int64_t ws_size, const void* bias, void* out, int out_dtype, int64_t M, int64_t N,
-                 int64_t K, bool gelu, hipStream_t stream) {
+                 int64_t ws_size, const void* bias, const Residual* res, void* out, int out_dtype,
+                 int64_t M, int64_t N, int64_t K, bool gelu, hipStream_t stream) {
+    const Residual r = res ? *res : Residual{nullptr, 0, nullptr};
     const int g = gelu ? 1 : 0;
     switch (out_dtype) {
-        case W8A8_BF16: gemv_dispatch<W8A8_BF16>(q, w, xs, ws, ws_size, bias, out, M, N, K, g, stream); break;
-        case W8A8_F16: gemv_dispatch<W8A8_F16>(q, w, xs, ws, ws_size, bias, out, M, N, K, g, stream); break;
-        default: gemv_dispatch<W8A8_F32>(q, w, xs, ws, ws_size, bias, out, M, N, K, g, stream); break;
+        case W8A8_BF16: gemv_dispatch<W8A8_BF16>(q, w, xs, ws, ws_size, bias, r, out, M, N, K, g, stream); break;
+        case W8A8_F16: gemv_dispatch<W8A8_F16>(q, w, xs, ws, ws_size, bias, r, out, M, N, K, g, stream); break;
+        default: gemv_dispatch<W8A8_F32>(q, w, xs, ws, ws_size, bias, r, out, M, N, K, g, stream); break;
     }
 }
 

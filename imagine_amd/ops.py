@@ -7,8 +7,9 @@ selection, argument conversions and error classes/messages follow
 HIP kernels of libw8a8_hip.so; torch only allocates tensors, converts dtypes
 of small operands (scales, bias) and supplies the current stream.
 
-Not built here (raise NotImplementedError): ConvRot rotation, and the
-SwiGLU / SiTU / RMSNorm input activations.
+The residual kwargs are fused into the GEMM / GEMV epilogue (or applied by
+the HIP residual kernel).  Not built here (raise NotImplementedError):
+ConvRot rotation, and the SwiGLU / SiTU / RMSNorm input activations.
 """
 import torch
 
@@ -153,6 +154,42 @@ def gemm_dequant_xq(x, xs, w, ws, bias, out_dtype, gelu=False, out=None):
     return out
 
 
+def _residual_operands(residual, scale, m, n, device, dtype):
+    """The crate's conversions of the residual operands (cuda_linear.rs:707-722,
+    int8_linear.rs:99-111): both in the output dtype, residual [M, N], scale flat."""
+    r = residual.to(device=device, dtype=dtype).reshape(m, n).contiguous()
+    s = scale.to(device=device, dtype=dtype).reshape(-1).contiguous()
+    return r, s
+
+
+def gemm_dequant_residual(q, w, xs, ws, bias, out_dtype, residual, residual_scale, out=None):
+    """INT8 GEMM + dequant + the pre-norm block's residual in one epilogue (the
+    reference's ``cutlass_int8_dequant_residual``)."""
+    _require_cuda(q, w, xs, ws, bias)
+    M, K = q.shape
+    N = w.shape[0]
+    r, rs = _residual_operands(residual, residual_scale, M, N, q.device, out_dtype)
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=q.device)
+    _lib.check(_lib.load().w8a8_gemm_dequant_residual(
+        _ptr(q), _ptr(w), _ptr(xs), _ptr(ws), ws.numel(), _ptr(bias), _ptr(rs), rs.numel(), _ptr(r),
+        _ptr(out), _dtype_code(out_dtype, "INT8 linear output"), M, N, K, 0, _stream(q.device)))
+    return out
+
+
+def gemv_dequant_residual(q, w, xs, ws, bias, out_dtype, residual, residual_scale):
+    """M = 1 / 2 GEMV + dequant + residual (``int8_gemv_dequant`` with residual)."""
+    _require_cuda(q, w, xs, ws, bias)
+    M, K = q.shape
+    N = w.shape[0]
+    r, rs = _residual_operands(residual, residual_scale, M, N, q.device, out_dtype)
+    out = torch.empty((M, N), dtype=out_dtype, device=q.device)
+    _lib.check(_lib.load().w8a8_gemv_dequant_residual(
+        _ptr(q), _ptr(w), _ptr(xs), _ptr(ws), ws.numel(), _ptr(bias), _ptr(rs), rs.numel(), _ptr(r),
+        _ptr(out), _dtype_code(out_dtype, "GEMV output"), M, N, K, 0, _stream(q.device)))
+    return out
+
+
 def dequantize_linear(acc, xs, ws, bias, out_dtype, gelu=False):
     """Standalone int32 -> out dequant (the reference's ``dequantize_int8_linear``)."""
     _require_cuda(acc, xs, ws, bias)
@@ -182,12 +219,23 @@ def route(m, k, n):
 
 
 def apply_residual(out, residual, scale):
-    """int8_linear.rs:99-111: residual.to(out).addcmul(out, scale.to(out))."""
+    """int8_linear.rs:99-111: residual.to(out).addcmul(out, scale.to(out)), in
+    place on ``out`` by the HIP residual kernel (one fma per element, as the
+    reference's GPU addcmul)."""
     if residual is None:
         return out
     if scale is None:
         raise ValueError("residual requires residual_scale")
-    return residual.to(out.dtype).addcmul(out, scale.to(out.dtype))
+    _require_cuda(out)
+    out2 = out.reshape(-1, out.shape[-1])
+    if not out2.is_contiguous():
+        raise ValueError("apply_residual needs a contiguous output")
+    m, n = out2.shape
+    r, rs = _residual_operands(residual, scale, m, n, out.device, out.dtype)
+    _lib.check(_lib.load().w8a8_residual_apply(
+        _ptr(out2), _ptr(r), _ptr(rs), rs.numel(), _dtype_code(out.dtype, "residual"), m, n,
+        _stream(out.device)))
+    return out
 
 
 def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=False,
@@ -236,12 +284,19 @@ def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=Fals
     flags = (_lib.SCALE_RECIP if scale_form == "recip" else 0) | (
         _lib.ACT_GELU_TANH if input_act == "gelu_tanh" else 0) | (
         _lib.FUSED_QUANT if fused_quant else 0)
-    _lib.check(lib.w8a8_int8_linear(
-        _ptr(x2), _dtype_code(x2.dtype, "INT8 quantization"), _ptr(weight), _ptr(ws), ws.numel(),
-        _ptr(b), _ptr(out), out_code, m, n, k, flags, _ptr(workspace), workspace.numel(),
-        _stream(x.device)))
-    if residual is not None:
-        out = apply_residual(out, residual.reshape(out.shape), residual_scale)
+    if residual is None:
+        _lib.check(lib.w8a8_int8_linear(
+            _ptr(x2), _dtype_code(x2.dtype, "INT8 quantization"), _ptr(weight), _ptr(ws), ws.numel(),
+            _ptr(b), _ptr(out), out_code, m, n, k, flags, _ptr(workspace), workspace.numel(),
+            _stream(x.device)))
+    else:
+        # fused into the epilogue: the reference's CUTLASS / M = 1 residual
+        # routes and its eager addcmul round alike (one fma)
+        r, rs = _residual_operands(residual, residual_scale, m, n, x.device, out_dtype)
+        _lib.check(lib.w8a8_int8_linear_residual(
+            _ptr(x2), _dtype_code(x2.dtype, "INT8 quantization"), _ptr(weight), _ptr(ws), ws.numel(),
+            _ptr(b), _ptr(rs), rs.numel(), _ptr(r), _ptr(out), out_code, m, n, k, flags,
+            _ptr(workspace), workspace.numel(), _stream(x.device)))
     if len(shape) == 2:
         return out
     return out.reshape(*shape[:-1], n)

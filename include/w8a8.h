@@ -94,6 +94,31 @@ int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const f
                       int64_t ws_size, const void* bias, void* out, int out_dtype,
                       int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream);
 
+/* GEMM with the fused residual epilogue of the pre-norm block:
+ *   lin[m,n] = O(fma(float(sum_k q[m,k] w[n,k]) * xs[m], ws[n], bias[n]))
+ *   out[m,n] = O(fma(lin[m,n], rscale[n], resid[m,n]))
+ * Replaces Kitchen `cutlass_int8_dequant_residual` (archived
+ * cutlass_gemm_int8.cu:122-188), called at cuda_linear.rs:724-742; the same
+ * single fma as the crate's eager apply_residual on the GPU (int8_linear.rs:99-111).
+ * rscale (rscale_size 1 or N entries) and resid ([M, N]) are in the output
+ * dtype.  No flags (an output activation or int32 output is rejected). */
+int w8a8_gemm_dequant_residual(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                               int64_t ws_size, const void* bias, const void* rscale,
+                               int64_t rscale_size, const void* resid, void* out, int out_dtype,
+                               int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream);
+
+/* M = 1 or 2 GEMV with the same residual epilogue.  Replaces `int8_gemv_dequant`
+ * with its residual arguments (cuda_linear.rs:657-676; gemv_residual_args :171-191). */
+int w8a8_gemv_dequant_residual(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
+                               int64_t ws_size, const void* bias, const void* rscale,
+                               int64_t rscale_size, const void* resid, void* out, int out_dtype,
+                               int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream);
+
+/* In place: out[m,n] = O(fma(out[m,n], rscale[n], resid[m,n])), all in dtype.
+ * Replaces the eager apply_residual (inference/src/int8_linear.rs:99-111). */
+int w8a8_residual_apply(void* out, const void* resid, const void* rscale, int64_t rscale_size,
+                        int dtype, int64_t M, int64_t N, hipStream_t stream);
+
 /* GEMM that quantizes the activation inside its tile load: x is the float
  * activation and xs its row scales from w8a8_row_scales (same flags).  Output
  * is bit-identical to w8a8_quantize_rowwise followed by w8a8_gemm_dequant.
@@ -124,6 +149,17 @@ int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* w
                      int64_t ws_size, const void* bias, void* out, int out_dtype,
                      int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
                      int64_t workspace_bytes, hipStream_t stream);
+
+/* w8a8_int8_linear with the residual of the pre-norm block (the crate's
+ * residual / residual_scale kwargs, cuda_linear.rs:700-744 and the eager
+ * fallback int8_linear.rs:99-111), fused into the GEMM or GEMV epilogue:
+ * out = O(fma(linear(x), rscale[n], resid[m,n])), rscale and resid in the
+ * output dtype. */
+int w8a8_int8_linear_residual(const void* x, int x_dtype, const int8_t* w, const float* ws,
+                              int64_t ws_size, const void* bias, const void* rscale,
+                              int64_t rscale_size, const void* resid, void* out, int out_dtype,
+                              int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
+                              int64_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

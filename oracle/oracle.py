@@ -38,6 +38,7 @@ def lib():
         f.w8o_quant_rowwise.argtypes = [p, i32, i64, i64, i32, i32, p, p]
         f.w8o_gemm_i32.argtypes = [p, p, i64, i64, i64, p]
         f.w8o_epilogue_kitchen.argtypes = [p, p, p, i64, p, p, i32, i64, i64, i32, i32]
+        f.w8o_residual.argtypes = [p, p, p, i64, i32, i64, i64, i32]
         f.w8o_epilogue_eager.argtypes = [p, p, p, i64, p, p, i32, i64, i64]
         f.w8o_gelu_tanh_tensor.argtypes = [p, p, i32, i64]
         f.w8o_f32_to_bf16_n.argtypes = [p, p, i64]
@@ -144,6 +145,17 @@ def gelu_tanh(x, dtype):
     y = np.empty_like(x)
     lib().w8o_gelu_tanh_tensor(_ptr(x), _ptr(y), DTYPE_CODE[dtype], x.size)
     return y
+
+
+def residual(out, resid, rscale, dtype, contract=1):
+    """out' = O(resid + out * rscale) in the output dtype (w8o_residual); all
+    three in storage convention of ``dtype``; rscale of 1 or N entries."""
+    out = np.ascontiguousarray(out).copy()
+    m, n = out.shape
+    resid = np.ascontiguousarray(resid, dtype=out.dtype).reshape(m, n)
+    rscale = np.ascontiguousarray(rscale, dtype=out.dtype).reshape(-1)
+    lib().w8o_residual(_ptr(out), _ptr(resid), _ptr(rscale), rscale.size, DTYPE_CODE[dtype], m, n, contract)
+    return out
 
 
 def linear_kitchen(x, x_dtype, w, ws, bias, out_dtype, scale_mode=0, input_act=0,

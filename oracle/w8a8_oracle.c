@@ -24,6 +24,8 @@
  *   w8o_epilogue_kitchen reference CUDA payloads (GEMM/GEMV/M1 routes, all dtypes).
  *   w8o_epilogue_eager   reference eager_int8_linear CPU payloads.
  *   w8o_gelu_tanh        reference gelu_tanh activation payloads (1 bf16 ulp).
+ *   w8o_residual         reference CUDA residual payloads (fused, unaligned and
+ *                        eager residual modes of the GEMM, GEMV and M=1 routes).
  */
 #include <math.h>
 #include <stdint.h>
@@ -239,6 +241,28 @@ void w8o_epilogue_eager(const int32_t* acc, const float* xs, const float* ws, in
 }
 
 /* Element-wise gelu_tanh on a tensor of the given dtype, result rounded to it. */
+/* Residual step after the linear's output rounding, in the output dtype:
+ *   out[m,n] = O( float(resid[m,n]) + float(out[m,n]) * float(rscale[n]) )
+ * contract = 1: one fused multiply-add (a single fp32 rounding before O);
+ * contract = 0: the product is rounded to fp32 before the add.
+ * The reference's fused CUTLASS form (archived cutlass_gemm_int8.cu:122-188:
+ * Add2 rounds the linear to the output type, Mul3 / Add4 in fp32, then O) and
+ * its eager apply_residual (inference/src/int8_linear.rs:99-111: residual
+ * .to(out).addcmul(out, scale.to(out))).  rscale has rs_size 1 or N entries;
+ * resid is [M, N].  All three tensors are in the output dtype. */
+void w8o_residual(void* out, const void* resid, const void* rscale, int64_t rs_size, int dtype,
+                  int64_t M, int64_t N, int contract) {
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t n = 0; n < N; ++n) {
+            float o = load_as_f32(out, dtype, m * N + n);
+            float r = load_as_f32(resid, dtype, m * N + n);
+            float s = load_as_f32(rscale, dtype, rs_size == 1 ? 0 : n);
+            float v = contract ? fmaf(o, s, r) : (r + o * s);
+            store_from_f32(out, dtype, m * N + n, v);
+        }
+    }
+}
+
 void w8o_gelu_tanh_tensor(const void* x, void* y, int dtype, int64_t count) {
     for (int64_t i = 0; i < count; ++i)
         store_from_f32(y, dtype, i, w8o_gelu_tanh(load_as_f32(x, dtype, i)));

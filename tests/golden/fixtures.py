@@ -10,7 +10,7 @@ from . import operands as OP
 
 PATH = Path(__file__).resolve().parent / "kitchen_int8_fixtures.json.gz"
 
-# Modes that need the residual epilogue (not part of the linear family built here).
+# Modes that carry the pre-norm residual (residual + residual_scale).
 RESIDUAL_MODES = {"residual", "fused_residual", "unaligned_residual", "unaligned_residual_scale"}
 SECTIONS = {
     "cuda_int8_gemm": OP.gemm_operands,
@@ -25,15 +25,18 @@ def load():
     return json.load(gzip.open(PATH))
 
 
-def linear_cases(section, with_errors=False):
+def linear_cases(section, with_errors=False, residual=False):
     """Non-ConvRot end-to-end cases of a CUDA section whose activation is None or
-    gelu_tanh and that need no residual.  Yields (case, operands)."""
+    gelu_tanh: without a residual, or (residual=True) only the residual modes.
+    Yields (case, operands)."""
     for c in load()[section]:
         if c.get("convrot"):
             continue
         if c.get("activation") not in (None, "gelu_tanh"):
             continue
-        if c["mode"] in RESIDUAL_MODES or (section == "cuda_int8_activation" and c["mode"] == "full"):
+        if section == "cuda_int8_activation" and c["mode"] == "full":
+            continue
+        if (c["mode"] in RESIDUAL_MODES) != residual:
             continue
         if ("error" in c) != with_errors:
             continue

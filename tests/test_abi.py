@@ -60,6 +60,23 @@ def test_argument_errors_return_reference_codes_and_messages():
     # operator: workspace too small
     rc, msg = _err(lib.w8a8_int8_linear(None, 2, None, None, 1, None, None, 2, 4, 16, 64, 0, None, 10, None))
     assert rc == _lib.ERR_VALUE and "workspace" in msg
+    # residual entries: a residual without its scale (int8_linear.rs:107), a
+    # scale of neither 1 nor N entries, and an output activation with a residual
+    buf = ctypes.c_void_p(16)  # never dereferenced: every call below fails its checks first
+    rc, msg = _err(lib.w8a8_gemm_dequant_residual(None, None, None, None, 1, None, None, 1, buf, None, 2,
+                                                  4, 8, 64, 0, None))
+    assert rc == _lib.ERR_VALUE and msg == "residual requires residual_scale"
+    rc, msg = _err(lib.w8a8_gemm_dequant_residual(None, None, None, None, 1, None, buf, 3, buf, None, 2,
+                                                  4, 8, 64, 0, None))
+    assert rc == _lib.ERR_RUNTIME and "residual_scale" in msg
+    rc, _ = _err(lib.w8a8_gemv_dequant_residual(None, None, None, None, 1, None, buf, 1, buf, None, 2,
+                                                1, 8, 64, _lib.ACT_GELU_TANH, None))
+    assert rc == _lib.ERR_VALUE
+    rc, msg = _err(lib.w8a8_residual_apply(buf, None, buf, 1, 2, 4, 8, None))
+    assert rc == _lib.ERR_VALUE and msg == "residual requires residual_scale"
+    rc, msg = _err(lib.w8a8_int8_linear_residual(None, 2, None, None, 1, None, buf, 5, buf, None, 2, 4, 8,
+                                                 64, 0, None, 0, None))
+    assert rc == _lib.ERR_RUNTIME and "residual_scale" in msg
     # empty outputs are a no-op success, nothing launched
     assert lib.w8a8_gemm_dequant(None, None, None, None, 1, None, None, 2, 0, 16, 64, 0, None) == 0
     assert lib.w8a8_quantize_rowwise(None, 2, None, None, 0, 64, 0, None) == 0

@@ -338,6 +338,93 @@ def test_dequantize_linear_gelu_within_one_ulp():
     _gelu_close(storage(out, "bf16"), want, "bf16")
 
 
+def _residual_inputs(m, n, odt, seed):
+    g = torch.Generator().manual_seed(seed)
+    resid = (torch.randn(m, n, generator=g) * 2.0).to(TD[odt])
+    rscale = (torch.rand(n, generator=g) * 1.5 + 0.25).to(TD[odt])
+    return resid, rscale
+
+
+@pytest.mark.parametrize("odt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("rs_scalar", [False, True])
+@pytest.mark.parametrize("shape", [(300, 512, 768), (11712, 3072, 3072)])
+def test_gemm_residual_epilogue_bit_exact(odt, rs_scalar, shape):
+    """GEMM + dequant + residual, bit for bit against the oracle's
+    O(fma(O(lin), rscale, resid)) on the whole output (full size: the out-proj
+    shape of the DiT block)."""
+    m, n, k = shape
+    if m > 1000 and odt != "bf16":
+        pytest.skip("full size checked for bf16 only")
+    x = make_x(m, k, "bf16", seed=31)
+    q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    w = make_w(n, k, seed=32)
+    ws = (torch.rand(n, generator=torch.Generator().manual_seed(33)) * 9e-3 + 1e-3).float()
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(34)) * 0.02).to(TD[odt])
+    resid, rscale = _residual_inputs(m, n, odt, 35)
+    if rs_scalar:
+        rscale = rscale[:1]
+    out = W.gemm_dequant_residual(torch.from_numpy(q_ref).to(DEV), w.to(DEV), torch.from_numpy(xs_ref).to(DEV),
+                                  ws.to(DEV), bias.to(DEV), TD[odt], resid.to(DEV), rscale.to(DEV))
+    lin = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt), odt)
+    want = O.residual(lin, storage(resid, odt), storage(rscale, odt), odt)
+    assert np.array_equal(storage(out, odt), want)
+
+
+def test_gemm_residual_unaligned_operands_take_the_direct_epilogue():
+    """A residual and a scale that are not 16-byte aligned (the reference's
+    unaligned_residual / unaligned_residual_scale modes) give the same bits."""
+    m, n, k = 200, 264, 512
+    x = make_x(m, k, "bf16", seed=41)
+    q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    w = make_w(n, k, seed=42)
+    ws = torch.full((n,), 0.004)
+    resid, rscale = _residual_inputs(m, n, "bf16", 43)
+    rbuf = torch.empty(m * n + 1, dtype=torch.bfloat16, device=DEV)
+    rbuf[1:] = resid.reshape(-1).to(DEV)
+    sbuf = torch.empty(n + 3, dtype=torch.bfloat16, device=DEV)
+    sbuf[3:] = rscale.to(DEV)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    # device operands are held in names for the whole call: a temporary's
+    # memory could be handed to the next temporary before the launch reads it
+    qd, wd = torch.from_numpy(q_ref).to(DEV), w.to(DEV)
+    xsd, wsd = torch.from_numpy(xs_ref).to(DEV), ws.to(DEV)
+    lib = W._lib.load()
+    W._lib.check(lib.w8a8_gemm_dequant_residual(
+        qd.data_ptr(), wd.data_ptr(), xsd.data_ptr(), wsd.data_ptr(), n, None, sbuf[3:].data_ptr(), n,
+        rbuf[1:].data_ptr(), out.data_ptr(), W._lib.BF16, m, n, k, 0, torch.cuda.current_stream().cuda_stream))
+    lin = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), None, "bf16")
+    want = O.residual(lin, storage(resid, "bf16"), storage(rscale, "bf16"), "bf16")
+    assert np.array_equal(storage(out, "bf16"), want)
+
+
+@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("odt", ["bf16", "f32"])
+def test_gemv_residual_epilogue_bit_exact(m, odt):
+    n, k = 1536, 3072
+    x = make_x(m, k, "bf16", seed=51)
+    q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
+    w = make_w(n, k, seed=52)
+    ws = (torch.rand(n, generator=torch.Generator().manual_seed(53)) * 9e-3 + 1e-3).float()
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(54)) * 0.02).to(TD[odt])
+    resid, rscale = _residual_inputs(m, n, odt, 55)
+    out = W.gemv_dequant_residual(torch.from_numpy(q_ref).to(DEV), w.to(DEV), torch.from_numpy(xs_ref).to(DEV),
+                                  ws.to(DEV), bias.to(DEV), TD[odt], resid.to(DEV), rscale.to(DEV))
+    lin = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt), odt)
+    want = O.residual(lin, storage(resid, odt), storage(rscale, odt), odt)
+    assert np.array_equal(storage(out, odt), want)
+
+
+@pytest.mark.parametrize("odt", ["bf16", "f16", "f32"])
+def test_residual_apply_bit_exact(odt):
+    m, n = 37, 1000
+    g = torch.Generator().manual_seed(61)
+    out = (torch.randn(m, n, generator=g) * 3).to(TD[odt])
+    resid, rscale = _residual_inputs(m, n, odt, 62)
+    got = W.apply_residual(out.clone().to(DEV), resid.to(DEV), rscale.to(DEV))
+    want = O.residual(storage(out, odt), storage(resid, odt), storage(rscale, odt), odt)
+    assert np.array_equal(storage(got, odt), want)
+
+
 # ---------------------------------------------------------------- operator vs reference payloads
 
 
@@ -347,8 +434,10 @@ def _run_fixture(c, ops, scale_form, fused):
     w = torch.from_numpy(ops["weight"]).to(DEV)
     ws = torch.from_numpy(np.asarray(ops["scale"])).to(DEV)
     bias = None if ops["bias"] is None else torch.from_numpy(np.asarray(ops["bias"])).to(DEV)
-    out = W.int8_linear(x, w, ws, bias, TD[od], input_act=c.get("activation"),
-                        scale_form=scale_form, fused_quant=fused)
+    r = None if ops["residual"] is None else torch.from_numpy(np.asarray(ops["residual"])).to(DEV)
+    rs = None if ops["residual_scale"] is None else torch.from_numpy(np.asarray(ops["residual_scale"])).to(DEV)
+    out = W.int8_linear(x, w, ws, bias, TD[od], input_act=c.get("activation"), residual=r,
+                        residual_scale=rs, scale_form=scale_form, fused_quant=fused)
     assert list(out.shape) == c["output_shape"]
     return storage(out, od).reshape(-1), FX.payload(c, od)
 
@@ -362,6 +451,20 @@ def test_operator_reproduces_reference_cuda_payloads(section, scale_form):
         assert np.array_equal(got, want), c
         n += 1
     assert n > 100
+
+
+@pytest.mark.parametrize("section", ["cuda_int8_gemm", "cuda_int8_gemv", "cuda_int8_m1"])
+@pytest.mark.parametrize("fused", [False, True])
+def test_operator_reproduces_reference_residual_payloads(section, fused):
+    """Residual modes (fused, unaligned residual / scale, eager fallback) through
+    the operator, residual fused into the epilogue (or, with the fused
+    quantizer, applied by the residual kernel)."""
+    n = 0
+    for c, ops in FX.linear_cases(section, residual=True):
+        got, want = _run_fixture(c, ops, "ieee", fused=fused)
+        assert np.array_equal(got, want), c
+        n += 1
+    assert n >= 36
 
 
 def test_operator_fused_quant_reproduces_gemm_payloads():

@@ -187,6 +187,41 @@ def test_kitchen_route_linear_matches_reference_cuda_payloads(section):
     assert n > 100
 
 
+def _residual_case_outputs(section, contract):
+    """(got, want) per residual-mode CUDA case: the composed route, then the
+    residual step with the given rounding (oracle w8o_residual)."""
+    for c, ops in FX.linear_cases(section, residual=True):
+        xd, od = OP.dtype_name(c["dtype"]), OP.dtype_name(c["output_dtype"])
+        x = O.to_dtype(ops["x"], xd)
+        x2 = x.reshape(-1, x.shape[-1])
+        ws = np.asarray(ops["scale"], np.float32).reshape(-1)
+        bias = None if ops["bias"] is None else O.to_dtype(np.asarray(ops["bias"], np.float32), od)
+        out, _, _, _ = O.linear_kitchen(x2, xd, ops["weight"], ws, bias, od)
+        r = O.to_dtype(np.asarray(ops["residual"], np.float32).reshape(out.shape), od)
+        s = O.to_dtype(np.asarray(ops["residual_scale"], np.float32).reshape(-1), od)
+        yield c, O.residual(out, r, s, od, contract=contract).reshape(-1), FX.payload(c, od)
+
+
+@pytest.mark.parametrize("section", ["cuda_int8_gemm", "cuda_int8_gemv", "cuda_int8_m1"])
+def test_residual_matches_reference_cuda_payloads(section):
+    """O(fma(O(lin), rscale, resid)) reproduces every residual-mode payload of
+    the reference (fused CUTLASS residual, unaligned residual / scale, and the
+    eager fallback on the GEMM, GEMV and M=1 routes)."""
+    n = 0
+    for c, got, want in _residual_case_outputs(section, contract=1):
+        assert np.array_equal(got, want), c
+        n += 1
+    assert n >= 36
+
+
+def test_residual_rounding_form_is_distinguished():
+    """The payloads tell the single-fma residual from a rounded product: the
+    fp32-output cases fail with the product rounded before the add."""
+    mismatched = sum(not np.array_equal(got, want)
+                     for _, got, want in _residual_case_outputs("cuda_int8_gemm", contract=0))
+    assert mismatched > 0
+
+
 def test_eager_route_linear_matches_reference_eager_payloads():
     """reference_int8_linear.py: eager int8_linear on CPU (IEEE scale) and on a
     CUDA device (torch's CUDA division by a scalar multiplies by the reciprocal,
