@@ -5,10 +5,10 @@ Drop-in for the reference crate's ``int8_linear`` operator
 (inference/src/cuda_linear.rs:311-317).
 """
 from . import _lib
-from .ops import (apply_residual, dequantize_linear, gemm_dequant, gemm_dequant_residual, gemm_dequant_xq,
-                  gemm_i32, gemv_dequant, gemv_dequant_residual, int8_linear, quantize_rowwise, route,
-                  row_scales)
+from .ops import (apply_residual, convrot_rotate, dequantize_linear, gemm_dequant, gemm_dequant_residual,
+                  gemm_dequant_xq, gemm_i32, gemv_dequant, gemv_dequant_residual, int8_linear, quantize_rowwise,
+                  quantize_rowwise_convrot, route, row_scales)
 
 __all__ = ["int8_linear", "quantize_rowwise", "row_scales", "gemv_dequant", "gemv_dequant_residual",
            "gemm_dequant", "gemm_dequant_residual", "gemm_dequant_xq", "gemm_i32", "dequantize_linear",
-           "apply_residual", "route", "_lib"]
+           "apply_residual", "convrot_rotate", "quantize_rowwise_convrot", "route", "_lib"]

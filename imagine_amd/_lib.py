@@ -37,6 +37,12 @@ SIGNATURES = {
     "w8a8_residual_apply": (_i, [_p, _p, _p, _i64, _i, _i64, _i64, _p]),
     "w8a8_int8_linear_residual": (_i, [_p, _i, _p, _p, _i64, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64,
                                        _u32, _p, _i64, _p]),
+    "w8a8_convrot_rotate": (_i, [_p, _i, _p, _i64, _i64, _i64, _p]),
+    "w8a8_convrot_workspace_bytes": (_i64, [_i64, _i64, _i64, _i]),
+    "w8a8_quantize_rowwise_convrot": (_i, [_p, _i, _p, _p, _i64, _i64, _i64, _u32, _p, _i64, _p]),
+    "w8a8_int8_linear_convrot_workspace_bytes": (_i64, [_i64, _i64, _i64, _i]),
+    "w8a8_int8_linear_convrot": (_i, [_p, _i, _p, _p, _i64, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _i64,
+                                      _u32, _p, _i64, _p]),
 }
 
 _lib = None

@@ -27,6 +27,11 @@ bool launch_gemm_xq(const void* x, int x_dtype, const float* xs, const int8_t* w
 void launch_dequant(const int32_t* acc, const float* xs, const float* ws, int64_t ws_size,
                     const void* bias, void* out, int out_dtype, int64_t M, int64_t N, bool gelu,
                     hipStream_t stream);
+bool convrot_fused_route(int64_t K, int64_t group);
+void launch_convrot_quant(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M, int64_t K,
+                          bool recip, hipStream_t stream);
+void launch_convrot_rotate(const void* x, int x_dtype, void* y, int64_t M, int64_t K, int64_t G,
+                           hipStream_t stream);
 }  // namespace w8a8
 
 namespace {
@@ -65,6 +70,18 @@ int check_ws(int64_t ws_size, int64_t N, const char* msg) {
 }
 
 // Residual operands of the fused residual epilogue (cuda_linear.rs:707-744).
+// The reference builds its Hadamard matrix first (int8_utils.rs:36-46) and
+// then splits the features into groups (:60-73), with these messages.
+int check_convrot_group(int64_t K, int64_t group) {
+    if (group < 4 || (group & (group - 1)) != 0 || (group & 0x5555555555555555ll) == 0)
+        return fail(W8A8_ERR_VALUE, "Regular Hadamard size must be a power of 4, got " + std::to_string(group));
+    if (K % group != 0)
+        return fail(W8A8_ERR_VALUE, "features " + std::to_string(K) + " not divisible by group_size " +
+                                        std::to_string(group));
+    if (group > 16384) return fail(W8A8_ERR_RUNTIME, "ConvRot groups above 16384 are not supported");
+    return W8A8_OK;
+}
+
 int check_residual(const void* rscale, int64_t rscale_size, const void* resid, int64_t N) {
     if (!rscale || !resid) return fail(W8A8_ERR_VALUE, "residual requires residual_scale");
     if (rscale_size != 1 && rscale_size != N)
@@ -216,6 +233,53 @@ int64_t w8a8_int8_linear_workspace_bytes(int64_t M, int64_t K) {
     return (M * K + 255) / 256 * 256 + M * 4;
 }
 
+int64_t w8a8_convrot_workspace_bytes(int64_t M, int64_t K, int64_t group, int x_dtype) {
+    if (M < 0 || K < 0 || !valid_dtype(x_dtype)) return -1;
+    if (w8a8::convrot_fused_route(K, group)) return 0;
+    return M * K * (x_dtype == W8A8_F32 ? 4 : 2);
+}
+
+int w8a8_convrot_rotate(const void* x, int x_dtype, void* y, int64_t M, int64_t K, int64_t group,
+                        hipStream_t stream) {
+    if (M < 0 || K < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (int rc = check_convrot_group(K, group)) return rc;
+    if (!valid_dtype(x_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for ConvRot rotation");
+    if (M == 0 || K == 0) return W8A8_OK;
+    if (!x || !y) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    w8a8::launch_convrot_rotate(x, x_dtype, y, M, K, group, stream);
+    return check_launch("convrot_rotate");
+}
+
+int w8a8_quantize_rowwise_convrot(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M, int64_t K,
+                                  int64_t group, uint32_t flags, void* rotated, int64_t rotated_bytes,
+                                  hipStream_t stream) {
+    if (int rc = check_common(M, 0, K, flags)) return rc;
+    if (flags & ~W8A8_SCALE_RECIP)
+        return fail(W8A8_ERR_VALUE, "the ConvRot quantizer takes only W8A8_SCALE_RECIP");
+    if (int rc = check_convrot_group(K, group)) return rc;
+    if (!valid_dtype(x_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for INT8 quantization");
+    if (M == 0) return W8A8_OK;
+    if (K > 0 && (!x || !q)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (!xs) return fail(W8A8_ERR_VALUE, "null scale pointer");
+    const bool recip = flags & W8A8_SCALE_RECIP;
+    if (K == 0) return w8a8_quantize_rowwise(x, x_dtype, q, xs, M, K, flags, stream);
+    if (w8a8::convrot_fused_route(K, group)) {
+        w8a8::launch_convrot_quant(x, x_dtype, q, xs, M, K, recip, stream);
+        return check_launch("quantize_int8_rowwise_convrot");
+    }
+    if (!rotated || rotated_bytes < w8a8_convrot_workspace_bytes(M, K, group, x_dtype))
+        return fail(W8A8_ERR_VALUE, "rotated buffer smaller than w8a8_convrot_workspace_bytes(M, K, group, dtype)");
+    if (int rc = w8a8_convrot_rotate(x, x_dtype, rotated, M, K, group, stream)) return rc;
+    return w8a8_quantize_rowwise(rotated, x_dtype, q, xs, M, K, flags, stream);
+}
+
+int64_t w8a8_int8_linear_convrot_workspace_bytes(int64_t M, int64_t K, int64_t group, int x_dtype) {
+    const int64_t rot = w8a8_convrot_workspace_bytes(M, K, group, x_dtype);
+    if (rot < 0) return -1;
+    // q [M, K] int8 and xs [M] fp32, each padded to 256 bytes, then the rotated input
+    return (M * K + 255) / 256 * 256 + (M * 4 + 255) / 256 * 256 + rot;
+}
+
 }  // extern "C"
 
 namespace {
@@ -226,8 +290,8 @@ namespace {
 // applies it eagerly elsewhere, with the same single fma either way.
 int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
                      const void* bias, const w8a8::Residual* res, void* out, int out_dtype, int64_t M,
-                     int64_t N, int64_t K, uint32_t flags, void* workspace, int64_t workspace_bytes,
-                     hipStream_t stream) {
+                     int64_t N, int64_t K, int64_t convrot_group, uint32_t flags, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream) {
     if (int rc = check_common(M, N, K, flags)) return rc;
     if (flags & W8A8_OUT_INT32) return fail(W8A8_ERR_VALUE, "W8A8_OUT_INT32 is a GEMM-only flag");
     if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
@@ -243,10 +307,18 @@ int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* w
         return fail(W8A8_ERR_RUNTIME,
                     "INT8 GEMM not supported on this GPU for these dimensions (requires SM >= 7.5, "
                     "and dimensions multiple of 4).");
+    if (convrot_group) {
+        if (int rc = check_convrot_group(K, convrot_group)) return rc;
+        if (flags & W8A8_ACT_GELU_TANH)
+            return fail(W8A8_ERR_VALUE, "an input activation with ConvRot is not supported by this library");
+    }
     if (M == 0) return W8A8_OK;
-    const int64_t need = w8a8_int8_linear_workspace_bytes(M, K);
+    const int64_t need = convrot_group ? w8a8_int8_linear_convrot_workspace_bytes(M, K, convrot_group, x_dtype)
+                                       : w8a8_int8_linear_workspace_bytes(M, K);
     if (!workspace || workspace_bytes < need)
-        return fail(W8A8_ERR_VALUE, "workspace smaller than w8a8_int8_linear_workspace_bytes(M, K)");
+        return fail(W8A8_ERR_VALUE, convrot_group
+                                        ? "workspace smaller than w8a8_int8_linear_convrot_workspace_bytes"
+                                        : "workspace smaller than w8a8_int8_linear_workspace_bytes(M, K)");
     if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
         return fail(W8A8_ERR_VALUE, "workspace must be 256-byte aligned");
     int8_t* q = static_cast<int8_t*>(workspace);
@@ -257,7 +329,7 @@ int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* w
     // Fused route: row scales, then a GEMM that quantizes its activation tiles
     // (an input activation is only applied by the standalone quantizer); a
     // residual is then applied by the standalone residual kernel.
-    if (!gemv && (flags & W8A8_FUSED_QUANT) && !(qflags & W8A8_ACT_GELU_TANH) && N > 0 &&
+    if (!convrot_group && !gemv && (flags & W8A8_FUSED_QUANT) && !(qflags & W8A8_ACT_GELU_TANH) && N > 0 &&
         x_dtype != W8A8_F32 && K % 16 == 0) {
         if (int rc = w8a8_row_scales(x, x_dtype, xs, M, K, qflags, stream)) return rc;
         if (w8a8::launch_gemm_xq(x, x_dtype, xs, w, ws, ws_size, bias, out, out_dtype, M, N, K,
@@ -267,7 +339,15 @@ int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* w
             return w8a8_residual_apply(out, res->resid, res->rscale, res->rs_size, out_dtype, M, N, stream);
         }
     }
-    if (int rc = w8a8_quantize_rowwise(x, x_dtype, q, xs, M, K, qflags, stream)) return rc;
+    if (convrot_group) {
+        void* rotated = static_cast<char*>(workspace) + (M * K + 255) / 256 * 256 + (M * 4 + 255) / 256 * 256;
+        if (int rc = w8a8_quantize_rowwise_convrot(x, x_dtype, q, xs, M, K, convrot_group, qflags, rotated,
+                                                   w8a8_convrot_workspace_bytes(M, K, convrot_group, x_dtype),
+                                                   stream))
+            return rc;
+    } else if (int rc = w8a8_quantize_rowwise(x, x_dtype, q, xs, M, K, qflags, stream)) {
+        return rc;
+    }
     if (N == 0) return W8A8_OK;
     if (res) {
         if (gemv)
@@ -287,7 +367,7 @@ extern "C" {
 int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
                      const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
                      uint32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, nullptr, out, out_dtype, M, N, K, flags,
+    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, nullptr, out, out_dtype, M, N, K, 0, flags,
                             workspace, workspace_bytes, stream);
 }
 
@@ -297,8 +377,17 @@ int w8a8_int8_linear_residual(const void* x, int x_dtype, const int8_t* w, const
                               int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
                               int64_t workspace_bytes, hipStream_t stream) {
     const w8a8::Residual res{rscale, rscale_size, resid};
-    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, &res, out, out_dtype, M, N, K, flags,
+    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, &res, out, out_dtype, M, N, K, 0, flags,
                             workspace, workspace_bytes, stream);
+}
+
+int w8a8_int8_linear_convrot(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
+                             const void* bias, const void* rscale, int64_t rscale_size, const void* resid,
+                             void* out, int out_dtype, int64_t M, int64_t N, int64_t K, int64_t group,
+                             uint32_t flags, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    const w8a8::Residual res{rscale, rscale_size, resid};
+    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, resid ? &res : nullptr, out, out_dtype, M, N, K,
+                            group, flags, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,332 @@
+// ConvRot activation quantization for gfx950: a regular Hadamard rotation of
+// every `group`-wide slice of a token row, then per-token absmax INT8.
+//
+// Replaces Kitchen's quantize_int8_rowwise_convrot64_kernel
+// (native/comfy-port/kitchen/int8_linear.cu:1204-1314, launcher :1609-1719)
+// for the fused route and rotate_activation + quantize_int8_rowwise
+// (inference/src/convrot.rs:474-484, int8_utils.rs:97-106) for the others.
+//
+// Rotation: y = x_g . H_G, H_G = (H4 (x) ... (x) H4) / sqrt(G),
+// H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] (int8_utils.rs:21-58),
+// computed as radix-4 stages at strides 1, 4, 16, 64 in fp32, each output
+// 0.5 * (x0 + x1 + x2 - x3) (or a sign variant) with its operands added left
+// to right: the fused reference kernel's operation order (int8_linear.cu:881-895).
+//
+// Fused route (group 256, K % 256 == 0, 256 <= K <= 16384): the rotated
+// values stay in fp32 for the row's absmax and are rounded to the input dtype
+// T only for the quotient, q = clamp(rint(T(T(y) / T(s)))).
+// Rotate route (any other power-of-4 group): y is rounded to T and written
+// out; the plain per-token quantizer then runs on it.
+//
+// Layout of the fast kernels: each lane holds 64 consecutive elements of a
+// group (digits d0, d1, d2 of the in-group index d3*64 + d2*16 + d1*4 + d0),
+// so the first three stages run in registers; the four lanes of a quad hold
+// d3 = 0..3 of one 256-group, and the last stage reads them with DPP quad
+// broadcasts.  A row never leaves registers between its absmax and quantize
+// passes.
+#include "w8a8_common.h"
+
+namespace w8a8 {
+
+constexpr int kRotGroup = 256;   // the fused route's group
+constexpr int kLaneElems = 64;   // consecutive elements per lane
+
+// 0.5 * (H4 row k) . (x0, x1, x2, x3), in place, operands left to right.
+__device__ __forceinline__ void h4_stage(float& a, float& b, float& c, float& d) {
+    const float x0 = a, x1 = b, x2 = c, x3 = d;
+    a = 0.5f * (x0 + x1 + x2 - x3);
+    b = 0.5f * (x0 + x1 - x2 + x3);
+    c = 0.5f * (x0 - x1 + x2 + x3);
+    d = 0.5f * (-x0 + x1 + x2 + x3);
+}
+
+// Value of v in lane K of this lane's quad (DPP quad_perm [K,K,K,K]).
+template <int K>
+__device__ __forceinline__ float quad_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xf, 0xf, false));
+}
+
+// Stage across the quad: lane d of the quad gets 0.5 * (H4 row d) . (x0..x3),
+// x_k being v of quad lane k.  sg[k] is -1 where row d of H4 has its minus
+// sign (k == 3 - d), else +1; the products are exact, so fma(x, sg, t) is the
+// reference's t +- x.
+__device__ __forceinline__ float h4_across_quad(float v, const float (&sg)[4]) {
+    const float x0 = quad_lane<0>(v), x1 = quad_lane<1>(v), x2 = quad_lane<2>(v), x3 = quad_lane<3>(v);
+    float t = x0 * sg[0];
+    t = fmaf(x1, sg[1], t);
+    t = fmaf(x2, sg[2], t);
+    t = fmaf(x3, sg[3], t);
+    return 0.5f * t;
+}
+
+// The in-register stages of a lane's 64 elements: strides 1, 4, 16, as many
+// as the group has (G = 4, 16, 64 or more).
+template <int G>
+__device__ __forceinline__ void lane_stages(float (&v)[kLaneElems]) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) h4_stage(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    if constexpr (G >= 16) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int d0 = 0; d0 < 4; ++d0) {
+                const int b = 16 * a + d0;
+                h4_stage(v[b], v[b + 4], v[b + 8], v[b + 12]);
+            }
+    }
+    if constexpr (G >= 64) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) h4_stage(v[r], v[r + 16], v[r + 32], v[r + 48]);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void load_lane(const void* src, bool ok, float (&v)[kLaneElems]) {
+    using D = DType<DT>;
+    constexpr int E = 16 / D::bytes;  // elements per 16-byte chunk
+    const uint4* p = static_cast<const uint4*>(src);
+#pragma unroll
+    for (int c = 0; c < kLaneElems / E; ++c) {
+        const uint4 raw = ok ? p[c] : make_uint4(0, 0, 0, 0);
+        const typename D::storage* e = reinterpret_cast<const typename D::storage*>(&raw);
+#pragma unroll
+        for (int i = 0; i < E; ++i) v[c * E + i] = D::load(e[i]);
+    }
+}
+
+// Fused route.  A block holds rows_per_block rows of ngroups 256-groups, one
+// quad per group; quads past the block's rows (or past M) compute on zeros
+// and store nothing, so every lane takes part in the DPP stage and the barrier.
+template <int DT>
+__global__ __launch_bounds__(1024) void convrot_quant_rows(const void* __restrict__ xv,
+                                                           int8_t* __restrict__ q,
+                                                           float* __restrict__ xs, int64_t M,
+                                                           int K, int rows_per_block, int recip) {
+    using D = DType<DT>;
+    extern __shared__ float group_amax[];  // one per quad
+    const int ngroups = K / kRotGroup;
+    const int quad = threadIdx.x / 4;
+    const int d3 = threadIdx.x % 4;
+    const int rb = quad / ngroups;
+    const int g = quad - rb * ngroups;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * rows_per_block + rb;
+    const bool active = rb < rows_per_block && row < M;
+    const int64_t col = static_cast<int64_t>(g) * kRotGroup + d3 * kLaneElems;
+
+    float v[kLaneElems];
+    load_lane<DT>(static_cast<const char*>(xv) + ((active ? row : 0) * K + col) * D::bytes, active, v);
+    lane_stages<kRotGroup>(v);
+    float sg[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sg[k] = (k == 3 - d3) ? -1.0f : 1.0f;
+    float m = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kLaneElems; ++r) {
+        v[r] = h4_across_quad(v[r], sg);
+        m = fmaxf(m, fabsf(v[r]));
+    }
+    // quad max: quad_perm [1,0,3,2] then [2,3,0,1]
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0xb1, 0xf, 0xf, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x4e, 0xf, 0xf, false)));
+    if (d3 == 0) group_amax[quad] = m;
+    __syncthreads();
+    if (!active) return;
+
+    float amax = 0.0f;
+    const float* ga = group_amax + rb * ngroups;
+    for (int i = 0; i < ngroups; ++i) amax = fmaxf(amax, ga[i]);
+    const float s = row_scale<DT>(amax, recip != 0);
+    if (g == 0 && d3 == 0) xs[row] = s;
+    const RowQuant rq = row_quant<DT>(s);
+    uint32_t packed[kLaneElems / 4];
+#pragma unroll
+    for (int j = 0; j < kLaneElems / 4; ++j)
+        packed[j] = pack4_low_bytes(quant_byte<DT>(D::round(v[4 * j]), rq), quant_byte<DT>(D::round(v[4 * j + 1]), rq),
+                                    quant_byte<DT>(D::round(v[4 * j + 2]), rq),
+                                    quant_byte<DT>(D::round(v[4 * j + 3]), rq));
+    uint4* dst = reinterpret_cast<uint4*>(q + row * K + col);
+#pragma unroll
+    for (int c = 0; c < kLaneElems / 16; ++c)
+        dst[c] = make_uint4(packed[4 * c], packed[4 * c + 1], packed[4 * c + 2], packed[4 * c + 3]);
+}
+
+// Fused route, any alignment: one block per row, the rotated row in LDS
+// (K <= 16384 floats), stage by stage like the reference kernel.
+template <int DT>
+__global__ __launch_bounds__(256) void convrot_quant_rows_generic(const void* __restrict__ xv,
+                                                                  int8_t* __restrict__ q,
+                                                                  float* __restrict__ xs, int64_t M,
+                                                                  int K, int recip) {
+    using D = DType<DT>;
+    extern __shared__ float rowbuf[];
+    __shared__ float part[4];
+    const int64_t row = blockIdx.x;
+    const typename D::storage* x = static_cast<const typename D::storage*>(xv) + row * K;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) rowbuf[k] = D::load(x[k]);
+    __syncthreads();
+    for (int S = 1; S < kRotGroup; S *= 4) {
+        for (int b = threadIdx.x; b < K / 4; b += blockDim.x) {
+            const int j = b % (kRotGroup / 4);
+            float* p = rowbuf + (b / (kRotGroup / 4)) * kRotGroup + (j % S) + (j / S) * 4 * S;
+            h4_stage(p[0], p[S], p[2 * S], p[3 * S]);
+        }
+        __syncthreads();
+    }
+    float amax = 0.0f;
+    for (int k = threadIdx.x; k < K; k += blockDim.x) amax = fmaxf(amax, fabsf(rowbuf[k]));
+    amax = wave_max(amax);
+    if ((threadIdx.x % kWave) == 0) part[threadIdx.x / kWave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    const float s = row_scale<DT>(amax, recip != 0);
+    if (threadIdx.x == 0) xs[row] = s;
+    const RowQuant rq = row_quant<DT>(s);
+    for (int k = threadIdx.x; k < K; k += blockDim.x)
+        q[row * K + k] = static_cast<int8_t>(quant_elem<DT>(D::round(rowbuf[k]), rq));
+}
+
+// Rotate route, aligned rows with K % 64 == 0 and G <= 256: every lane
+// rotates 64 consecutive elements (with its quad for G = 256) and stores them
+// rounded to T.
+template <int DT, int G>
+__global__ __launch_bounds__(256) void convrot_rotate_vec(const void* __restrict__ xv,
+                                                          void* __restrict__ yv, int64_t chunks) {
+    using D = DType<DT>;
+    constexpr int E = 16 / D::bytes;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const bool ok = c < chunks;
+    float v[kLaneElems];
+    load_lane<DT>(static_cast<const char*>(xv) + (ok ? c : 0) * kLaneElems * D::bytes, ok, v);
+    lane_stages<G>(v);
+    float sg[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sg[k] = (k == 3 - static_cast<int>(threadIdx.x % 4)) ? -1.0f : 1.0f;
+    uint4* dst = reinterpret_cast<uint4*>(static_cast<char*>(yv) + (ok ? c : 0) * kLaneElems * D::bytes);
+    // G = 256: the quad stage chunk by chunk, each chunk stored as it is done
+    // (keeps the live registers to one chunk of stage outputs)
+#pragma unroll
+    for (int k = 0; k < kLaneElems / E; ++k) {
+        if constexpr (G == kRotGroup) {
+#pragma unroll
+            for (int i = 0; i < E; ++i) v[k * E + i] = h4_across_quad(v[k * E + i], sg);
+        }
+        uint4 out;
+        uint32_t* w = reinterpret_cast<uint32_t*>(&out);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if constexpr (DT == W8A8_F32) w[i] = __float_as_uint(v[k * E + i]);
+            else w[i] = D::store2(v[k * E + 2 * i], v[k * E + 2 * i + 1]);
+        }
+        if (ok) dst[k] = out;
+    }
+}
+
+// Rotate route, any power-of-4 group up to 16384 and any alignment: one block
+// per group of the [M, K] tensor (groups are contiguous), the group in LDS.
+template <int DT>
+__global__ __launch_bounds__(256) void convrot_rotate_generic(const void* __restrict__ xv,
+                                                              void* __restrict__ yv, int64_t K,
+                                                              int G) {
+    using D = DType<DT>;
+    extern __shared__ float gbuf[];
+    // block b: row b / (K / G), group b % (K / G), i.e. element offset b * G
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * G;
+    const typename D::storage* x = static_cast<const typename D::storage*>(xv) + base;
+    typename D::storage* y = static_cast<typename D::storage*>(yv) + base;
+    for (int i = threadIdx.x; i < G; i += blockDim.x) gbuf[i] = D::load(x[i]);
+    __syncthreads();
+    for (int S = 1; S < G; S *= 4) {
+        for (int b = threadIdx.x; b < G / 4; b += blockDim.x) {
+            float* p = gbuf + (b % S) + (b / S) * 4 * S;
+            h4_stage(p[0], p[S], p[2 * S], p[3 * S]);
+        }
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < G; i += blockDim.x) y[i] = D::store(gbuf[i]);
+}
+
+// ---------------------------------------------------------------- host side
+
+bool convrot_fused_route(int64_t K, int64_t group) {
+    return group == kRotGroup && K % kRotGroup == 0 && K >= kRotGroup && K <= 16384;
+}
+
+// Rows per block of the fused kernel: whole waves with every quad busy where
+// possible (ngroups * rows % 16 == 0), about 256 threads, at most 1024.
+static int fused_rows_per_block(int ngroups) {
+    int best = 1;
+    double best_util = 0.0;
+    for (int r = 1; 4 * r * ngroups <= 1024; ++r) {
+        const int threads = 4 * r * ngroups;
+        const int padded = (threads + kWave - 1) / kWave * kWave;
+        const double util = static_cast<double>(threads) / padded;
+        if (util > best_util + 1e-9) {
+            best = r;
+            best_util = util;
+        }
+        if (util > 1.0 - 1e-9 && threads >= 256) return r;
+    }
+    return best;
+}
+
+template <int DT>
+static void launch_fused(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, bool recip,
+                         hipStream_t stream) {
+    constexpr int E = 16 / DType<DT>::bytes;
+    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0;
+    static_assert(kLaneElems % E == 0, "lane chunks");
+    if (aligned) {
+        const int ngroups = static_cast<int>(K / kRotGroup);
+        const int rpb = fused_rows_per_block(ngroups);
+        const int threads = (4 * rpb * ngroups + kWave - 1) / kWave * kWave;
+        const int quads = threads / 4;
+        const dim3 grid(static_cast<unsigned>((M + rpb - 1) / rpb));
+        hipLaunchKernelGGL((convrot_quant_rows<DT>), grid, dim3(threads), quads * sizeof(float), stream, x, q,
+                           xs, M, static_cast<int>(K), rpb, recip ? 1 : 0);
+    } else {
+        // the row in LDS: up to 64 KB beside the kernel's static 16 bytes
+        const size_t lds = K * sizeof(float);
+        if (lds > 32 * 1024)
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&convrot_quant_rows_generic<DT>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        hipLaunchKernelGGL((convrot_quant_rows_generic<DT>), dim3(static_cast<unsigned>(M)), dim3(256), lds,
+                           stream, x, q, xs, M, static_cast<int>(K), recip ? 1 : 0);
+    }
+}
+
+void launch_convrot_quant(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M, int64_t K,
+                          bool recip, hipStream_t stream) {
+    if (x_dtype == W8A8_BF16) launch_fused<W8A8_BF16>(x, q, xs, M, K, recip, stream);
+    else if (x_dtype == W8A8_F16) launch_fused<W8A8_F16>(x, q, xs, M, K, recip, stream);
+    else launch_fused<W8A8_F32>(x, q, xs, M, K, recip, stream);
+}
+
+template <int DT>
+static void launch_rotate_dt(const void* x, void* y, int64_t M, int64_t K, int64_t G, hipStream_t stream) {
+    const bool vec = G <= kRotGroup && K % kLaneElems == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    if (vec) {
+        const int64_t chunks = M * K / kLaneElems;
+        const dim3 grid(static_cast<unsigned>((chunks + 255) / 256));
+        if (G == 4) hipLaunchKernelGGL((convrot_rotate_vec<DT, 4>), grid, dim3(256), 0, stream, x, y, chunks);
+        else if (G == 16) hipLaunchKernelGGL((convrot_rotate_vec<DT, 16>), grid, dim3(256), 0, stream, x, y, chunks);
+        else if (G == 64) hipLaunchKernelGGL((convrot_rotate_vec<DT, 64>), grid, dim3(256), 0, stream, x, y, chunks);
+        else hipLaunchKernelGGL((convrot_rotate_vec<DT, 256>), grid, dim3(256), 0, stream, x, y, chunks);
+        return;
+    }
+    const size_t lds = G * sizeof(float);
+    if (lds > 32 * 1024)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&convrot_rotate_generic<DT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    const dim3 grid(static_cast<unsigned>(M * (K / G)));
+    hipLaunchKernelGGL((convrot_rotate_generic<DT>), grid, dim3(256), lds, stream, x, y, K, static_cast<int>(G));
+}
+
+void launch_convrot_rotate(const void* x, int x_dtype, void* y, int64_t M, int64_t K, int64_t G,
+                           hipStream_t stream) {
+    if (x_dtype == W8A8_BF16) launch_rotate_dt<W8A8_BF16>(x, y, M, K, G, stream);
+    else if (x_dtype == W8A8_F16) launch_rotate_dt<W8A8_F16>(x, y, M, K, G, stream);
+    else launch_rotate_dt<W8A8_F32>(x, y, M, K, G, stream);
+}
+
+}  // namespace w8a8

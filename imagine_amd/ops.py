@@ -8,8 +8,11 @@ HIP kernels of libw8a8_hip.so; torch only allocates tensors, converts dtypes
 of small operands (scales, bias) and supplies the current stream.
 
 The residual kwargs are fused into the GEMM / GEMV epilogue (or applied by
-the HIP residual kernel).  Not built here (raise NotImplementedError):
-ConvRot rotation, and the SwiGLU / SiTU / RMSNorm input activations.
+the HIP residual kernel).  ``convrot`` rotates the activations by the regular
+Hadamard matrix of ``convrot_groupsize`` before quantizing them (fused into
+the quantizer on the crate's fused route).  Not built here (raise
+NotImplementedError): the SwiGLU / SiTU / RMSNorm input activations, and an
+input activation combined with ConvRot.
 """
 import torch
 
@@ -84,6 +87,39 @@ def quantize_rowwise(x, scale_form="ieee", input_act=None):
     _lib.check(_lib.load().w8a8_quantize_rowwise(
         _ptr(x), _dtype_code(x.dtype, "INT8 quantization"), _ptr(q), _ptr(s), M, K, flags,
         _stream(x.device)))
+    return q, s
+
+
+def convrot_rotate(x, group=256):
+    """Regular Hadamard rotation of every ``group``-wide slice of the rows of a
+    [M, K] device tensor, rounded to its dtype: the crate's rotate_activation
+    (int8_utils.rs:97-106)."""
+    _require_cuda(x)
+    x = _as_2d(x)
+    M, K = x.shape
+    y = torch.empty_like(x)
+    _lib.check(_lib.load().w8a8_convrot_rotate(_ptr(x), _dtype_code(x.dtype, "ConvRot rotation"), _ptr(y), M, K,
+                                               group, _stream(x.device)))
+    return y
+
+
+def quantize_rowwise_convrot(x, group=256, scale_form="ieee"):
+    """ConvRot activation quantization -> (q int8 [M, K], s fp32 [M, 1]) by the
+    crate's route (cuda_linear.rs:586-599): fused rotation + quantization for
+    group 256 and 256 <= K <= 16384 (Kitchen quantize_int8_rowwise_convrot64,
+    int8_linear.cu:1204-1314), else rotate then quantize."""
+    _require_cuda(x)
+    x = _as_2d(x)
+    M, K = x.shape
+    code = _dtype_code(x.dtype, "INT8 quantization")
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    rot_bytes = lib.w8a8_convrot_workspace_bytes(M, K, group, code)
+    rotated = torch.empty(max(rot_bytes, 1), dtype=torch.uint8, device=x.device) if rot_bytes > 0 else None
+    flags = _lib.SCALE_RECIP if scale_form == "recip" else 0
+    _lib.check(lib.w8a8_quantize_rowwise_convrot(_ptr(x), code, _ptr(q), _ptr(s), M, K, group, flags,
+                                                 _ptr(rotated), max(rot_bytes, 0), _stream(x.device)))
     return q, s
 
 
@@ -253,10 +289,10 @@ def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=Fals
     """
     if residual is not None and residual_scale is None:
         raise ValueError("int8_linear: residual requires residual_scale")
-    if convrot:
-        raise NotImplementedError("ConvRot activation rotation is not part of this build")
     if input_act not in (None, "gelu_tanh"):
         raise NotImplementedError(f"input_act {input_act!r} is not part of this build")
+    if convrot and input_act is not None:
+        raise NotImplementedError("an input activation combined with ConvRot is not part of this build")
     _require_cuda(x, weight)
     out_dtype = x.dtype if out_dtype is None else out_dtype
     shape = x.shape
@@ -278,15 +314,27 @@ def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=Fals
     b = _bias(bias, x.device, out_dtype)
     out = torch.empty((m, n), dtype=out_dtype, device=x.device)
     lib = _lib.load()
-    need = lib.w8a8_int8_linear_workspace_bytes(m, k)
+    x_code = _dtype_code(x2.dtype, "INT8 quantization")
+    if convrot:
+        need = lib.w8a8_int8_linear_convrot_workspace_bytes(m, k, convrot_groupsize, x_code)
+    else:
+        need = lib.w8a8_int8_linear_workspace_bytes(m, k)
     if workspace is None or workspace.numel() < need or workspace.data_ptr() % 256 != 0:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
     flags = (_lib.SCALE_RECIP if scale_form == "recip" else 0) | (
         _lib.ACT_GELU_TANH if input_act == "gelu_tanh" else 0) | (
         _lib.FUSED_QUANT if fused_quant else 0)
-    if residual is None:
+    if convrot:
+        r = rs = None
+        if residual is not None:
+            r, rs = _residual_operands(residual, residual_scale, m, n, x.device, out_dtype)
+        _lib.check(lib.w8a8_int8_linear_convrot(
+            _ptr(x2), x_code, _ptr(weight), _ptr(ws), ws.numel(), _ptr(b), _ptr(rs),
+            0 if rs is None else rs.numel(), _ptr(r), _ptr(out), out_code, m, n, k, convrot_groupsize, flags,
+            _ptr(workspace), workspace.numel(), _stream(x.device)))
+    elif residual is None:
         _lib.check(lib.w8a8_int8_linear(
-            _ptr(x2), _dtype_code(x2.dtype, "INT8 quantization"), _ptr(weight), _ptr(ws), ws.numel(),
+            _ptr(x2), x_code, _ptr(weight), _ptr(ws), ws.numel(),
             _ptr(b), _ptr(out), out_code, m, n, k, flags, _ptr(workspace), workspace.numel(),
             _stream(x.device)))
     else:
@@ -294,7 +342,7 @@ def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=Fals
         # routes and its eager addcmul round alike (one fma)
         r, rs = _residual_operands(residual, residual_scale, m, n, x.device, out_dtype)
         _lib.check(lib.w8a8_int8_linear_residual(
-            _ptr(x2), _dtype_code(x2.dtype, "INT8 quantization"), _ptr(weight), _ptr(ws), ws.numel(),
+            _ptr(x2), x_code, _ptr(weight), _ptr(ws), ws.numel(),
             _ptr(b), _ptr(rs), rs.numel(), _ptr(r), _ptr(out), out_code, m, n, k, flags,
             _ptr(workspace), workspace.numel(), _stream(x.device)))
     if len(shape) == 2:

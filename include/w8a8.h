@@ -161,6 +161,45 @@ int w8a8_int8_linear_residual(const void* x, int x_dtype, const int8_t* w, const
                               int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
                               int64_t workspace_bytes, hipStream_t stream);
 
+/* ---- ConvRot (online Hadamard rotation of the activations) ----------------
+ * Every `group`-wide slice of a row is multiplied by the regular Hadamard
+ * matrix H_G = (H4 (x) ... (x) H4) / sqrt(G) (inference/src/int8_utils.rs:21-58);
+ * group is a power of 4 up to 16384 that divides K.  Bad groups return
+ * W8A8_ERR_VALUE with the reference's messages (int8_utils.rs:36-46,60-73). */
+
+/* y = dtype(x rotated), [M, K] in x's dtype.  Replaces rotate_activation
+ * (int8_utils.rs:97-106) on the crate's unfused route (convrot.rs:474-484). */
+int w8a8_convrot_rotate(const void* x, int x_dtype, void* y, int64_t M, int64_t K, int64_t group,
+                        hipStream_t stream);
+
+/* Bytes of the rotated-input buffer w8a8_quantize_rowwise_convrot needs: 0 on
+ * the fused route (group 256, K % 256 == 0, 256 <= K <= 16384, the crate's
+ * predicate cuda_linear.rs:404-417), else M*K elements of x's dtype. */
+int64_t w8a8_convrot_workspace_bytes(int64_t M, int64_t K, int64_t group, int x_dtype);
+
+/* ConvRot activation quantization, by the crate's route (cuda_linear.rs:586-599):
+ * on the fused route it replaces Kitchen quantize_int8_rowwise_convrot64
+ * (native/comfy-port/kitchen/int8_linear.cu:1204-1314, launcher :1609-1719):
+ * fp32 rotation, absmax of the fp32 values, q = clamp(rint(T(T(y) / T(s));
+ * elsewhere it rotates into `rotated` (rounded to the dtype) and runs
+ * w8a8_quantize_rowwise on it.  Flags: W8A8_SCALE_RECIP. */
+int w8a8_quantize_rowwise_convrot(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M,
+                                  int64_t K, int64_t group, uint32_t flags, void* rotated,
+                                  int64_t rotated_bytes, hipStream_t stream);
+
+/* w8a8_int8_linear with convrot=true, convrot_groupsize=group (the crate's
+ * int8_linear kwargs, backend_signatures.rs:445-460; route cuda_linear.rs:586-599)
+ * and an optional residual (resid == NULL: none).  The workspace holds q, xs
+ * and, off the fused route, the rotated input:
+ * w8a8_int8_linear_convrot_workspace_bytes gives its size.  Input activations
+ * are not combined with ConvRot here (W8A8_ACT_GELU_TANH is refused). */
+int64_t w8a8_int8_linear_convrot_workspace_bytes(int64_t M, int64_t K, int64_t group, int x_dtype);
+int w8a8_int8_linear_convrot(const void* x, int x_dtype, const int8_t* w, const float* ws,
+                             int64_t ws_size, const void* bias, const void* rscale,
+                             int64_t rscale_size, const void* resid, void* out, int out_dtype,
+                             int64_t M, int64_t N, int64_t K, int64_t group, uint32_t flags,
+                             void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,8 @@ def lib():
         f.w8o_gemm_i32.argtypes = [p, p, i64, i64, i64, p]
         f.w8o_epilogue_kitchen.argtypes = [p, p, p, i64, p, p, i32, i64, i64, i32, i32]
         f.w8o_residual.argtypes = [p, p, p, i64, i32, i64, i64, i32]
+        f.w8o_convrot_rotate.argtypes = [p, i32, i64, i64, i64, p, p]
+        f.w8o_convrot_quant.argtypes = [p, i32, i64, i64, i64, i32, p, p, p]
         f.w8o_epilogue_eager.argtypes = [p, p, p, i64, p, p, i32, i64, i64]
         f.w8o_gelu_tanh_tensor.argtypes = [p, p, i32, i64]
         f.w8o_f32_to_bf16_n.argtypes = [p, p, i64]
@@ -91,6 +93,39 @@ def quant_rowwise(x, dtype, scale_mode=0, act=0):
     q = np.empty((M, K), np.int8)
     s = np.empty((M,), np.float32)
     lib().w8o_quant_rowwise(_ptr(x), DTYPE_CODE[dtype], M, K, scale_mode, act, _ptr(q), _ptr(s))
+    return q, s
+
+
+def convrot_fused_route(k, group):
+    """The reference's fused-rotation predicate (cuda_linear.rs:404-417):
+    group 256, K a multiple of 256 in [256, 16384]."""
+    return group == 256 and k % 256 == 0 and 256 <= k <= 16384
+
+
+def convrot_rotate(x, dtype, group):
+    """dtype(x rotated per `group`-wide slice) -> same shape and storage."""
+    x = np.ascontiguousarray(x, dtype=_storage(dtype))
+    M, K = x.shape
+    y = np.empty_like(x)
+    work = np.empty((group,), np.float32)
+    lib().w8o_convrot_rotate(_ptr(x), DTYPE_CODE[dtype], M, K, group, _ptr(y), _ptr(work))
+    return y
+
+
+def convrot_quant(x, dtype, group, scale_mode=0):
+    """ConvRot activation quantization of ``x`` [M, K] -> (q, s), by the route
+    the reference takes: the fused rotation (fp32 rotated values) where
+    ``convrot_fused_route`` holds, else rotate (rounded to the dtype) then
+    the plain per-token quantizer."""
+    x = np.ascontiguousarray(x, dtype=_storage(dtype))
+    M, K = x.shape
+    if not convrot_fused_route(K, group):
+        return quant_rowwise(convrot_rotate(x, dtype, group), dtype, scale_mode=scale_mode)
+    q = np.empty((M, K), np.int8)
+    s = np.empty((M,), np.float32)
+    work = np.empty((K,), np.float32)
+    lib().w8o_convrot_quant(_ptr(x), DTYPE_CODE[dtype], M, K, group, scale_mode, _ptr(q), _ptr(s),
+                            _ptr(work))
     return q, s
 
 
@@ -159,12 +194,15 @@ def residual(out, resid, rscale, dtype, contract=1):
 
 
 def linear_kitchen(x, x_dtype, w, ws, bias, out_dtype, scale_mode=0, input_act=0,
-                   epilogue_act=0, contract=1):
+                   epilogue_act=0, contract=1, convrot_group=0):
     """Composed GPU-route linear: quantize -> int32 GEMM -> single-rounding epilogue.
 
     Returns (out, q, xs, acc) so callers can check every intermediate.
     """
-    q, xs = quant_rowwise(x, x_dtype, scale_mode=scale_mode, act=input_act)
+    if convrot_group:
+        q, xs = convrot_quant(x, x_dtype, convrot_group, scale_mode=scale_mode)
+    else:
+        q, xs = quant_rowwise(x, x_dtype, scale_mode=scale_mode, act=input_act)
     acc = gemm_i32(q, w)
     out = epilogue_kitchen(acc, xs, ws, bias, out_dtype, contract=contract, act=epilogue_act)
     return out, q, xs, acc

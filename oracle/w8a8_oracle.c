@@ -26,6 +26,10 @@
  *   w8o_gelu_tanh        reference gelu_tanh activation payloads (1 bf16 ulp).
  *   w8o_residual         reference CUDA residual payloads (fused, unaligned and
  *                        eager residual modes of the GEMM, GEMV and M=1 routes).
+ *   w8o_convrot_*        reference ConvRot CUDA payloads (fused group-256 route
+ *                        and rotate-then-quantize route); the stage order against
+ *                        a dense float64 Hadamard matmul (H built by Kronecker
+ *                        products) and H.H^T = I.
  */
 #include <math.h>
 #include <stdint.h>
@@ -142,11 +146,39 @@ float w8o_gelu_tanh(float x) {
  * act 1 first applies gelu_tanh to x and rounds it to the dtype
  * (inference/src/int8_linear.rs:37-41 then :198-199).
  * x is [M, K] row-major; q is [M, K]; s is [M].  Finite inputs only. */
-void w8o_quant_rowwise(const void* x, int dtype, int64_t M, int64_t K, int scale_mode,
-                       int act, int8_t* q, float* s) {
+static float row_scale(float amax, int dtype, int scale_mode) {
     const float finite_max = dtype == W8O_F16 ? 65504.0f
                            : dtype == W8O_BF16 ? 3.38953139e38f : 3.40282347e38f;
+    float scale;
+    if (scale_mode == 1) {
+        float a = amax < finite_max ? amax : finite_max;
+        scale = a * (1.0f / 127.0f);
+    } else {
+        scale = amax / 127.0f;
+    }
+    if (!(scale >= 1e-30f)) scale = 1e-30f;
+    return scale;
+}
+
+/* dtype(s), with the eager rule that a scale rounding to zero becomes tiny(dtype). */
+static float scale_in_dtype(float scale, int dtype) {
     const float tiny = dtype == W8O_F16 ? 6.103515625e-5f : 1.17549435e-38f;
+    float sT = round_to(scale, dtype);
+    if (sT == 0.0f) sT = tiny;
+    return sT;
+}
+
+/* int8(clamp(round_half_even(dtype(v / sT)), -128, 127)); v already in dtype. */
+static int8_t quant_value(float v, float sT, int dtype) {
+    float quot = round_to(v / sT, dtype);
+    float r = rintf(quot); /* half-even in the default rounding mode */
+    if (r < -128.0f) r = -128.0f;
+    if (r > 127.0f) r = 127.0f;
+    return (int8_t)r;
+}
+
+void w8o_quant_rowwise(const void* x, int dtype, int64_t M, int64_t K, int scale_mode,
+                       int act, int8_t* q, float* s) {
     for (int64_t m = 0; m < M; ++m) {
         float amax = 0.0f;
         for (int64_t k = 0; k < K; ++k) {
@@ -155,26 +187,77 @@ void w8o_quant_rowwise(const void* x, int dtype, int64_t M, int64_t K, int scale
             float a = fabsf(v);
             if (a > amax) amax = a;
         }
-        float scale;
-        if (scale_mode == 1) {
-            float a = amax < finite_max ? amax : finite_max;
-            scale = a * (1.0f / 127.0f);
-        } else {
-            scale = amax / 127.0f;
-        }
-        if (!(scale >= 1e-30f)) scale = 1e-30f;
+        const float scale = row_scale(amax, dtype, scale_mode);
         s[m] = scale;
-        float sT = round_to(scale, dtype);
-        if (sT == 0.0f) sT = tiny;
+        const float sT = scale_in_dtype(scale, dtype);
         for (int64_t k = 0; k < K; ++k) {
             float v = load_as_f32(x, dtype, m * K + k);
             if (act == 1) v = round_to(w8o_gelu_tanh(v), dtype);
-            float quot = round_to(v / sT, dtype);
-            float r = rintf(quot); /* half-even in the default rounding mode */
-            if (r < -128.0f) r = -128.0f;
-            if (r > 127.0f) r = 127.0f;
-            q[m * K + k] = (int8_t)r;
+            q[m * K + k] = quant_value(v, sT, dtype);
         }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* ConvRot: a regular Hadamard rotation of every `group`-wide slice of a row,
+ * y = x_g . H_G with H_G = (H4 (x) H4 (x) ... (x) H4) / sqrt(G) and
+ * H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] (inference/src/
+ * int8_utils.rs:21-58, rotate_activation :97-106).  G is a power of 4.
+ *
+ * Computed the way the reference's fused CUDA quantizer does it
+ * (native/comfy-port/kitchen/int8_linear.cu:881-895 stages, :1270-1289 driver):
+ * radix-4 stages at strides 1, 4, 16, ... in fp32, every output
+ * 0.5f * (x0 + x1 + x2 - x3) (and the three other sign rows of H4) with the
+ * operands added left to right.  The 0.5 of each stage makes up 1/sqrt(G). */
+static void fht_group(float* v, int64_t G) {
+    for (int64_t S = 1; S < G; S *= 4) {
+        for (int64_t blk = 0; blk < G; blk += 4 * S) {
+            for (int64_t j = 0; j < S; ++j) {
+                float* p = v + blk + j;
+                const float x0 = p[0], x1 = p[S], x2 = p[2 * S], x3 = p[3 * S];
+                p[0] = 0.5f * (x0 + x1 + x2 - x3);
+                p[S] = 0.5f * (x0 + x1 - x2 + x3);
+                p[2 * S] = 0.5f * (x0 - x1 + x2 + x3);
+                p[3 * S] = 0.5f * (-x0 + x1 + x2 + x3);
+            }
+        }
+    }
+}
+
+/* Rotate-then-quantize route, rotation half (convrot.rs:474-484 with
+ * int8_utils.rs:97-106): y = dtype(rotation of x), [M, K] -> [M, K] in the
+ * same dtype.  `work` holds G floats. */
+void w8o_convrot_rotate(const void* x, int dtype, int64_t M, int64_t K, int64_t G, void* y,
+                        float* work) {
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t g = 0; g < K; g += G) {
+            for (int64_t i = 0; i < G; ++i) work[i] = load_as_f32(x, dtype, m * K + g + i);
+            fht_group(work, G);
+            for (int64_t i = 0; i < G; ++i) store_from_f32(y, dtype, m * K + g + i, work[i]);
+        }
+    }
+}
+
+/* Fused rotation + quantization (quantize_int8_rowwise_convrot64_kernel,
+ * native/comfy-port/kitchen/int8_linear.cu:1204-1314; G = 256):
+ *   y    = rotation of x in fp32, NOT rounded to the dtype
+ *   amax = max |y|;  s = scale of amax as in w8o_quant_rowwise (scale_mode)
+ *   q    = int8(clamp(round_half_even(dtype(dtype(y) / dtype(s))), -128, 127))
+ * (quant_div_float_to_float, int8_linear.cu:53-57).  `work` holds K floats. */
+void w8o_convrot_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t G,
+                       int scale_mode, int8_t* q, float* s, float* work) {
+    for (int64_t m = 0; m < M; ++m) {
+        float amax = 0.0f;
+        for (int64_t k = 0; k < K; ++k) work[k] = load_as_f32(x, dtype, m * K + k);
+        for (int64_t g = 0; g < K; g += G) fht_group(work + g, G);
+        for (int64_t k = 0; k < K; ++k) {
+            float a = fabsf(work[k]);
+            if (a > amax) amax = a;
+        }
+        const float scale = row_scale(amax, dtype, scale_mode);
+        s[m] = scale;
+        const float sT = scale_in_dtype(scale, dtype);
+        for (int64_t k = 0; k < K; ++k) q[m * K + k] = quant_value(round_to(work[k], dtype), sT, dtype);
     }
 }
 
@@ -240,7 +323,6 @@ void w8o_epilogue_eager(const int32_t* acc, const float* xs, const float* ws, in
     }
 }
 
-/* Element-wise gelu_tanh on a tensor of the given dtype, result rounded to it. */
 /* Residual step after the linear's output rounding, in the output dtype:
  *   out[m,n] = O( float(resid[m,n]) + float(out[m,n]) * float(rscale[n]) )
  * contract = 1: one fused multiply-add (a single fp32 rounding before O);
@@ -263,6 +345,7 @@ void w8o_residual(void* out, const void* resid, const void* rscale, int64_t rs_s
     }
 }
 
+/* Element-wise gelu_tanh on a tensor of the given dtype, result rounded to it. */
 void w8o_gelu_tanh_tensor(const void* x, void* y, int dtype, int64_t count) {
     for (int64_t i = 0; i < count; ++i)
         store_from_f32(y, dtype, i, w8o_gelu_tanh(load_as_f32(x, dtype, i)));

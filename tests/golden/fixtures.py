@@ -25,12 +25,13 @@ def load():
     return json.load(gzip.open(PATH))
 
 
-def linear_cases(section, with_errors=False, residual=False):
-    """Non-ConvRot end-to-end cases of a CUDA section whose activation is None or
-    gelu_tanh: without a residual, or (residual=True) only the residual modes.
+def linear_cases(section, with_errors=False, residual=False, convrot=False):
+    """End-to-end cases of a CUDA section whose activation is None or
+    gelu_tanh: without a residual, or (residual=True) only the residual modes;
+    non-ConvRot cases, or (convrot=True) only the ConvRot ones.
     Yields (case, operands)."""
     for c in load()[section]:
-        if c.get("convrot"):
+        if bool(c.get("convrot")) != convrot:
             continue
         if c.get("activation") not in (None, "gelu_tanh"):
             continue

@@ -77,6 +77,21 @@ def test_argument_errors_return_reference_codes_and_messages():
     rc, msg = _err(lib.w8a8_int8_linear_residual(None, 2, None, None, 1, None, buf, 5, buf, None, 2, 4, 8,
                                                  64, 0, None, 0, None))
     assert rc == _lib.ERR_RUNTIME and "residual_scale" in msg
+    # ConvRot groups: a power of 4 (int8_utils.rs:36-46) that divides K (:60-73)
+    for group in (0, 2, 8, 32, 48, -4):
+        rc, msg = _err(lib.w8a8_convrot_rotate(buf, 2, buf, 2, 256, group, None))
+        assert rc == _lib.ERR_VALUE and msg == f"Regular Hadamard size must be a power of 4, got {group}"
+    rc, msg = _err(lib.w8a8_quantize_rowwise_convrot(buf, 2, buf, buf, 2, 336, 64, 0, None, 0, None))
+    assert rc == _lib.ERR_VALUE and msg == "features 336 not divisible by group_size 64"
+    rc, msg = _err(lib.w8a8_quantize_rowwise_convrot(buf, 2, buf, buf, 2, 256, 64, 0, None, 0, None))
+    assert rc == _lib.ERR_VALUE and "rotated buffer" in msg  # off the fused route it needs the buffer
+    rc, _ = _err(lib.w8a8_int8_linear_convrot(buf, 2, buf, buf, 1, None, None, 0, None, buf, 2, 4, 8, 256, 256,
+                                              _lib.ACT_GELU_TANH, buf, 1 << 20, None))
+    assert rc == _lib.ERR_VALUE
+    assert lib.w8a8_convrot_workspace_bytes(4, 3072, 256, 2) == 0
+    assert lib.w8a8_convrot_workspace_bytes(4, 16640, 256, 2) == 4 * 16640 * 2
+    assert lib.w8a8_convrot_workspace_bytes(4, 256, 64, 0) == 4 * 256 * 4
+    assert lib.w8a8_int8_linear_convrot_workspace_bytes(3, 256, 64, 2) == 768 + 256 + 3 * 256 * 2
     # empty outputs are a no-op success, nothing launched
     assert lib.w8a8_gemm_dequant(None, None, None, None, 1, None, None, 2, 0, 16, 64, 0, None) == 0
     assert lib.w8a8_quantize_rowwise(None, 2, None, None, 0, 64, 0, None) == 0

@@ -425,10 +425,89 @@ def test_residual_apply_bit_exact(odt):
     assert np.array_equal(storage(got, odt), want)
 
 
+# ---------------------------------------------------------------- ConvRot
+
+CONVROT_SHAPES = [(37, 256), (5, 3072), (64, 3072), (3, 6144), (9, 12288), (2, 16384), (1, 4096)]
+
+
+def _convrot_check(x, dtype, group, scale_form):
+    q, s = W.quantize_rowwise_convrot(x, group, scale_form=scale_form)
+    q_ref, s_ref = O.convrot_quant(storage(x, dtype), dtype, group,
+                                   scale_mode=1 if scale_form == "recip" else 0)
+    assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+
+
+@pytest.mark.parametrize("scale_form", ["ieee", "recip"])
+@pytest.mark.parametrize("shape", CONVROT_SHAPES)
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_convrot_quant_fused_route_bit_exact(dtype, shape, scale_form):
+    """Fused rotation + quantization (group 256): codes and scales bit for bit
+    against the oracle, outlier-heavy rows included."""
+    m, k = shape
+    x = make_x(m, k, dtype, seed=71 + k, dist="student_t")
+    _convrot_check(x.to(DEV), dtype, 256, scale_form)
+
+
+def test_convrot_quant_full_size_bit_exact():
+    """11712 tokens x 3072 channels (the DiT block's activation), bf16."""
+    x = make_x(11712, 3072, "bf16", seed=73, dist="student_t")
+    _convrot_check(x.to(DEV), "bf16", 256, "ieee")
+
+
+@pytest.mark.parametrize("k", [3072, 16384])
+def test_convrot_quant_unaligned_input_bit_exact(k):
+    """An input that is not 16-byte aligned takes the row-in-LDS kernel."""
+    m = 3
+    x = make_x(m, k, "bf16", seed=75)
+    buf = torch.empty(m * k + 1, dtype=torch.bfloat16, device=DEV)
+    buf[1:] = x.reshape(-1).to(DEV)
+    _convrot_check(buf[1:].view(m, k), "bf16", 256, "recip")
+
+
+CONVROT_ROTATE_CASES = [(7, 256, 4), (7, 1024, 16), (5, 3072, 64), (3, 16640, 256), (2, 4096, 1024),
+                        (3, 48, 16), (4, 16640, 64), (2, 768, 256)]
+
+
+@pytest.mark.parametrize("m,k,group", CONVROT_ROTATE_CASES)
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_convrot_rotate_bit_exact(dtype, m, k, group):
+    x = make_x(m, k, dtype, seed=91 + group)
+    y = W.convrot_rotate(x.to(DEV), group)
+    assert np.array_equal(storage(y, dtype), O.convrot_rotate(storage(x, dtype), dtype, group))
+
+
+@pytest.mark.parametrize("m,k,group", [(4, 256, 64), (3, 16640, 256), (5, 1024, 16)])
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_convrot_quant_rotate_route_bit_exact(dtype, m, k, group):
+    x = make_x(m, k, dtype, seed=97 + k, dist="student_t")
+    _convrot_check(x.to(DEV), dtype, group, "recip")
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 512, 3072), (2, 1536, 3072), (1, 640, 4096), (64, 256, 16640)])
+def test_operator_convrot_equals_quantizer_then_linear(m, n, k):
+    """The ConvRot operator is the ConvRot quantizer followed by the GEMM/GEMV
+    with its epilogue, bit for bit, residual included."""
+    x = make_x(m, k, "bf16", seed=101).to(DEV)
+    w = make_w(n, k, seed=102).to(DEV)
+    ws = (torch.rand(n, generator=torch.Generator().manual_seed(103)) * 9e-3 + 1e-3).to(DEV)
+    bias = (torch.randn(n, generator=torch.Generator().manual_seed(104)) * 0.02).to(torch.bfloat16).to(DEV)
+    resid, rscale = _residual_inputs(m, n, "bf16", 105)
+    resid, rscale = resid.to(DEV), rscale.to(DEV)
+    out = W.int8_linear(x, w, ws, bias, torch.bfloat16, convrot=True, convrot_groupsize=256,
+                        residual=resid, residual_scale=rscale)
+    q, s = W.quantize_rowwise_convrot(x, 256)
+    if W.route(m, k, n) == "gemm":
+        want = W.gemm_dequant_residual(q, w, s, ws, bias, torch.bfloat16, resid, rscale)
+    else:
+        want = W.gemv_dequant_residual(q, w, s, ws, bias, torch.bfloat16, resid, rscale)
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+
+
 # ---------------------------------------------------------------- operator vs reference payloads
 
 
-def _run_fixture(c, ops, scale_form, fused):
+def _run_fixture(c, ops, scale_form, fused, convrot=False):
     xd, od = OP.dtype_name(c["dtype"]), OP.dtype_name(c["output_dtype"])
     x = from_storage(O.to_dtype(ops["x"], xd), xd)
     w = torch.from_numpy(ops["weight"]).to(DEV)
@@ -436,8 +515,9 @@ def _run_fixture(c, ops, scale_form, fused):
     bias = None if ops["bias"] is None else torch.from_numpy(np.asarray(ops["bias"])).to(DEV)
     r = None if ops["residual"] is None else torch.from_numpy(np.asarray(ops["residual"])).to(DEV)
     rs = None if ops["residual_scale"] is None else torch.from_numpy(np.asarray(ops["residual_scale"])).to(DEV)
-    out = W.int8_linear(x, w, ws, bias, TD[od], input_act=c.get("activation"), residual=r,
-                        residual_scale=rs, scale_form=scale_form, fused_quant=fused)
+    out = W.int8_linear(x, w, ws, bias, TD[od], convrot=convrot, convrot_groupsize=c.get("group", 256),
+                        input_act=c.get("activation"), residual=r, residual_scale=rs, scale_form=scale_form,
+                        fused_quant=fused)
     assert list(out.shape) == c["output_shape"]
     return storage(out, od).reshape(-1), FX.payload(c, od)
 
@@ -465,6 +545,29 @@ def test_operator_reproduces_reference_residual_payloads(section, fused):
         assert np.array_equal(got, want), c
         n += 1
     assert n >= 36
+
+
+@pytest.mark.parametrize("section", ["cuda_int8_gemm", "cuda_int8_gemv", "cuda_int8_m1", "cuda_int8_activation"])
+def test_operator_reproduces_reference_convrot_payloads(section):
+    """ConvRot cases without an input activation, with and without a residual,
+    through the operator with the CUDA scale form: bit for bit, except fp32
+    inputs off the fused route (the reference rotates those with a library
+    GEMM whose summation order is not restated), which agree within 2^-7."""
+    exact = close = 0
+    for residual in (False, True):
+        for c, ops in FX.linear_cases(section, residual=residual, convrot=True):
+            if c.get("activation"):
+                continue
+            got, want = _run_fixture(c, ops, "recip", fused=False, convrot=True)
+            od = OP.dtype_name(c["output_dtype"])
+            if OP.dtype_name(c["dtype"]) == "f32" and not O.convrot_fused_route(c["shape"][-1], c["group"]):
+                a, b = O.to_f32(got, od).astype(np.float64), O.to_f32(want, od).astype(np.float64)
+                assert np.abs(a - b).max() <= 2.0**-7 * np.abs(b).max(), c
+                close += 1
+            else:
+                assert np.array_equal(got, want), c
+                exact += 1
+    assert exact >= 60
 
 
 def test_operator_fused_quant_reproduces_gemm_payloads():

@@ -281,3 +281,111 @@ def test_gelu_tanh_within_one_bf16_ulp_of_aten_on_every_bf16_value():
     tol = np.abs(b) * 2.0**-7 + 2.0**-22
     assert (np.abs(a - b) <= tol).all()
     assert (ours == ref).mean() > 0.9999
+
+
+# ---------------------------------------------------------------- ConvRot
+
+
+def _hadamard_f64(G):
+    """int8_utils.rs:21-58 restated in float64: Kronecker powers of H4 over sqrt(G)."""
+    h4 = np.array([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], np.float64)
+    h = h4
+    while h.shape[0] < G:
+        h = np.kron(h, h4)
+    return h / np.sqrt(G)
+
+
+@pytest.mark.parametrize("G", [4, 16, 64, 256, 1024])
+def test_convrot_stages_equal_dense_hadamard_matmul(G):
+    """The radix-4 stage order computes x . H_G: against a float64 dense
+    product (fp32 rounding only), H_G orthogonal and symmetric, and rotating
+    twice gives x back."""
+    rng = np.random.default_rng(G)
+    x = rng.standard_normal((5, 2 * G)).astype(np.float32)
+    h = _hadamard_f64(G)
+    assert np.allclose(h @ h.T, np.eye(G), atol=1e-12) and np.array_equal(h, h.T)
+    want = (x.astype(np.float64).reshape(5, 2, G) @ h).reshape(5, 2 * G)
+    got = O.convrot_rotate(x, "f32", G)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    back = O.convrot_rotate(got, "f32", G)
+    assert np.abs(back - x).max() <= 1e-5 * np.abs(x).max()
+
+
+def test_convrot_stage_sign_rows_are_distinguished():
+    """A one-hot row picks out one row of H_256: the signs, positions and scale
+    of every output are those of the dense matrix (a transposed H4 or a wrong
+    stride fails here)."""
+    h = _hadamard_f64(256)
+    for i in (0, 1, 5, 17, 100, 255):
+        x = np.zeros((1, 256), np.float32)
+        x[0, i] = 1.0
+        assert np.array_equal(O.convrot_rotate(x, "f32", 256)[0], h[i].astype(np.float32))
+
+
+def test_convrot_route_predicate_matches_reference_native_calls():
+    """The fused route is taken exactly where the reference's captures called
+    quantize_int8_rowwise_convrot64 (GEMM and GEMV sections)."""
+    n = 0
+    for section in ("cuda_int8_gemm", "cuda_int8_gemv"):
+        for c in FX.load()[section]:
+            if not c.get("convrot") or "error" in c or not c.get("native_calls"):
+                continue
+            names = [nc["name"] if isinstance(nc, dict) else nc for nc in c["native_calls"]]
+            fused = "quantize_int8_rowwise_convrot64" in names
+            assert O.convrot_fused_route(c["shape"][-1], c["group"]) == fused, c
+            n += 1
+    assert n > 200
+
+
+def _convrot_case_outputs(section, scale_mode, residual):
+    for c, ops in FX.linear_cases(section, residual=residual, convrot=True):
+        if c.get("activation"):
+            continue
+        xd, od = OP.dtype_name(c["dtype"]), OP.dtype_name(c["output_dtype"])
+        x = O.to_dtype(ops["x"], xd)
+        x2 = x.reshape(-1, x.shape[-1])
+        ws = np.asarray(ops["scale"], np.float32).reshape(-1)
+        bias = None if ops["bias"] is None else O.to_dtype(np.asarray(ops["bias"], np.float32), od)
+        out, _, _, _ = O.linear_kitchen(x2, xd, ops["weight"], ws, bias, od, scale_mode=scale_mode,
+                                        convrot_group=c["group"])
+        if residual:
+            r = O.to_dtype(np.asarray(ops["residual"], np.float32).reshape(out.shape), od)
+            s = O.to_dtype(np.asarray(ops["residual_scale"], np.float32).reshape(-1), od)
+            out = O.residual(out, r, s, od)
+        yield c, xd, od, out.reshape(-1), FX.payload(c, od)
+
+
+def _library_summed_case(c, xd):
+    """fp32 inputs off the fused route: the reference rotates with its GEMM
+    library (x @ H in fp32), whose summation order is not restated here."""
+    return xd == "f32" and not O.convrot_fused_route(c["shape"][-1], c["group"])
+
+
+@pytest.mark.parametrize("section", ["cuda_int8_gemm", "cuda_int8_gemv", "cuda_int8_m1",
+                                     "cuda_int8_activation"])
+def test_convrot_linear_matches_reference_cuda_payloads(section):
+    """Every ConvRot payload without an input activation (with and without a
+    residual) bit for bit, with the CUDA scale form; fp32 inputs off the fused
+    route agree within 2^-7 relative (their rotation is a library GEMM)."""
+    exact = close = 0
+    for residual in (False, True):
+        for c, xd, od, got, want in _convrot_case_outputs(section, 1, residual):
+            if _library_summed_case(c, xd):
+                a, b = O.to_f32(got, od).astype(np.float64), O.to_f32(want, od).astype(np.float64)
+                assert np.abs(a - b).max() <= 2.0**-7 * np.abs(b).max(), c
+                close += 1
+            else:
+                assert np.array_equal(got, want), c
+                exact += 1
+    assert exact >= 60
+
+
+def test_convrot_scale_form_is_distinguished_on_the_rotate_route():
+    """The 16-bit rotate-route payloads need the CUDA scale form amax*(1/127):
+    the IEEE form misses some of them, while the fused route matches both."""
+    misses = {True: 0, False: 0}
+    for c, xd, od, got, want in _convrot_case_outputs("cuda_int8_gemm", 0, False):
+        if xd == "f32":
+            continue
+        misses[O.convrot_fused_route(c["shape"][-1], c["group"])] += not np.array_equal(got, want)
+    assert misses[True] == 0 and misses[False] > 0
