@@ -185,26 +185,21 @@ __device__ __forceinline__ RowQuant row_quant(float s) {
     return rq;
 }
 
-// RN(x / d) from the reciprocal: q0 = RN(x * r), remainder e = x - q0*d
-// (exact in one fma), corrected quotient RN(q0 + e * r).  With r = RN(1/d)
-// this is the correctly rounded quotient; that is verified exhaustively for
-// every bf16 and fp16 (x, d) pair a row can produce (tests/test_divide.py).
-// fp32 inputs use the hardware's IEEE division instead.
-__device__ __forceinline__ float div_rn(float x, const RowQuant& rq) {
-    float q0 = x * rq.r;
-    float e = fmaf(-q0, rq.d, x);
-    return fmaf(e, rq.r, q0);
+// The quotient as far as the int8 code needs it.  For 16-bit T the plain
+// product RN(x * RN(1/sT)) can differ from RN(x / sT) in the last fp32 bit,
+// but clamp(rint(T(.))) of the two is the same for every 16-bit x and every
+// reachable divisor (checked exhaustively, tests/divide_check.c); fp32 inputs
+// divide in IEEE.
+template <int DT>
+__device__ __forceinline__ float code_quotient(float x, const RowQuant& rq) {
+    if constexpr (DT == W8A8_F32) return x / rq.d;
+    else return DType<DT>::round(x * rq.r);
 }
 
 // One element: q = clamp(rint(T(x / sT)), -128, 127) as int.
 template <int DT>
 __device__ __forceinline__ int quant_elem(float x, const RowQuant& rq) {
-    float quot;
-    if constexpr (DT == W8A8_F32) {
-        quot = x / rq.d;
-    } else {
-        quot = DType<DT>::round(div_rn(x, rq));
-    }
+    const float quot = code_quotient<DT>(x, rq);
     float v = __builtin_rintf(quot);
     v = fminf(fmaxf(v, -128.0f), 127.0f);
     return static_cast<int>(v);
@@ -218,12 +213,7 @@ __device__ __forceinline__ int quant_elem(float x, const RowQuant& rq) {
 // bounds are integers), and NaN clamps to -128 in both forms.
 template <int DT>
 __device__ __forceinline__ uint32_t quant_byte(float x, const RowQuant& rq) {
-    float quot;
-    if constexpr (DT == W8A8_F32) {
-        quot = x / rq.d;
-    } else {
-        quot = DType<DT>::round(div_rn(x, rq));
-    }
+    const float quot = code_quotient<DT>(x, rq);
     const float v = fminf(fmaxf(quot, -128.0f), 127.0f);
     return __float_as_uint(v + 12582912.0f);
 }
@@ -233,6 +223,38 @@ __device__ __forceinline__ uint32_t pack4_low_bytes(uint32_t a, uint32_t b, uint
     const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);   // bytes: a0, b0, 0, 0
     const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x04000c0cu);   // bytes: 0, 0, c0, d0
     return ab | cd;
+}
+
+// Round two values to T and widen them back; bf16 rounds both in one
+// v_cvt_pk_bf16_f32 (the same bits as DType::round on each).
+template <int DT>
+__device__ __forceinline__ void round2(float& a, float& b) {
+    if constexpr (DT == W8A8_BF16) {
+        const uint32_t u = pack2_bf16(a, b);
+        a = __uint_as_float(u << 16);
+        b = __uint_as_float(u & 0xffff0000u);
+    } else {
+        a = DType<DT>::round(a);
+        b = DType<DT>::round(b);
+    }
+}
+
+// Four int8 codes packed (a lowest) for four values already in T: the same
+// codes as quant_byte, with the 16-bit quotient roundings done in pairs.
+template <int DT>
+__device__ __forceinline__ uint32_t quant4_packed(float a, float b, float c, float d, const RowQuant& rq) {
+    if constexpr (DT == W8A8_F32) {
+        return pack4_low_bytes(quant_byte<DT>(a, rq), quant_byte<DT>(b, rq), quant_byte<DT>(c, rq),
+                               quant_byte<DT>(d, rq));
+    } else {
+        float q0 = a * rq.r, q1 = b * rq.r, q2 = c * rq.r, q3 = d * rq.r;
+        round2<DT>(q0, q1);
+        round2<DT>(q2, q3);
+        auto byte = [](float q) {
+            return __float_as_uint(fminf(fmaxf(q, -128.0f), 127.0f) + 12582912.0f);
+        };
+        return pack4_low_bytes(byte(q0), byte(q1), byte(q2), byte(q3));
+    }
 }
 
 __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {

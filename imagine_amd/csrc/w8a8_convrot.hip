@@ -40,54 +40,76 @@ __device__ __forceinline__ void h4_stage(float& a, float& b, float& c, float& d)
     d = 0.5f * (-x0 + x1 + x2 + x3);
 }
 
-// Value of v in lane K of this lane's quad (DPP quad_perm [K,K,K,K]).
-template <int K>
-__device__ __forceinline__ float quad_lane(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xf, 0xf, false));
+// The fast kernels below leave out the 0.5 of every stage: a power-of-two
+// scale commutes with round-to-nearest while values stay normal, so their
+// stage outputs are exactly 2^L times the reference's (L stages) and the
+// factor 2^-L is applied once (folded into the quotient's divisor on the fused
+// route).  That holds for rows whose nonzero inputs lie within [2^-100, 2^120)
+// in magnitude (no sum then reaches a subnormal in the reference or overflows
+// here); the generic kernels keep the 0.5 per stage.
+//
+// (H4 row k) . (x0, x1, x2, x3) in place, operands left to right as above:
+// x0 + x1 is shared by rows 0 and 1, and row 3's (-x0 + x1) + x2 is
+// x2 - (x0 - x1) bit for bit (round-to-nearest-even is odd-symmetric).
+__device__ __forceinline__ void h4_sum(float& a, float& b, float& c, float& d) {
+    const float x0 = a, x1 = b, x2 = c, x3 = d;
+    const float p = x0 + x1, m = x0 - x1;
+    a = (p + x2) - x3;
+    b = (p - x2) + x3;
+    c = (m + x2) + x3;
+    d = (x2 - m) + x3;
 }
 
-// Stage across the quad: lane d of the quad gets 0.5 * (H4 row d) . (x0..x3),
-// x_k being v of quad lane k.  sg[k] is -1 where row d of H4 has its minus
-// sign (k == 3 - d), else +1; the products are exact, so fma(x, sg, t) is the
+// Value of v in lane K of this lane's quad (DPP quad_perm [K,K,K,K]; every
+// lane is active wherever this is used, so no source lane is ever invalid).
+// bound_ctrl lets the compiler fold the move into the consuming mul / fmac.
+template <int K>
+__device__ __forceinline__ float quad_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xf, 0xf, true));
+}
+
+// Stage across the quad: lane d of the quad gets (H4 row d) . (x0..x3), x_k
+// being v of quad lane k.  sg[k] is -1 where row d of H4 has its minus sign
+// (k == 3 - d), else +1; the products are exact, so fma(x, sg, t) is the
 // reference's t +- x.
-__device__ __forceinline__ float h4_across_quad(float v, const float (&sg)[4]) {
-    const float x0 = quad_lane<0>(v), x1 = quad_lane<1>(v), x2 = quad_lane<2>(v), x3 = quad_lane<3>(v);
-    float t = x0 * sg[0];
-    t = fmaf(x1, sg[1], t);
-    t = fmaf(x2, sg[2], t);
-    t = fmaf(x3, sg[3], t);
-    return 0.5f * t;
+__device__ __forceinline__ float h4_sum_across_quad(float v, const float (&sg)[4]) {
+    float t = quad_lane<0>(v) * sg[0];
+    t = fmaf(quad_lane<1>(v), sg[1], t);
+    t = fmaf(quad_lane<2>(v), sg[2], t);
+    return fmaf(quad_lane<3>(v), sg[3], t);
 }
 
 // The in-register stages of a lane's 64 elements: strides 1, 4, 16, as many
-// as the group has (G = 4, 16, 64 or more).
+// as the group has (G = 4, 16, 64 or more), unscaled.
 template <int G>
 __device__ __forceinline__ void lane_stages(float (&v)[kLaneElems]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) h4_stage(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    for (int j = 0; j < 16; ++j) h4_sum(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
     if constexpr (G >= 16) {
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
             for (int d0 = 0; d0 < 4; ++d0) {
                 const int b = 16 * a + d0;
-                h4_stage(v[b], v[b + 4], v[b + 8], v[b + 12]);
+                h4_sum(v[b], v[b + 4], v[b + 8], v[b + 12]);
             }
     }
     if constexpr (G >= 64) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) h4_stage(v[r], v[r + 16], v[r + 32], v[r + 48]);
+        for (int r = 0; r < 16; ++r) h4_sum(v[r], v[r + 16], v[r + 32], v[r + 48]);
     }
 }
 
+// 64 consecutive elements from a valid address (lanes without work of their
+// own read row 0, compute on it and store nothing).
 template <int DT>
-__device__ __forceinline__ void load_lane(const void* src, bool ok, float (&v)[kLaneElems]) {
+__device__ __forceinline__ void load_lane(const void* src, float (&v)[kLaneElems]) {
     using D = DType<DT>;
     constexpr int E = 16 / D::bytes;  // elements per 16-byte chunk
     const uint4* p = static_cast<const uint4*>(src);
 #pragma unroll
     for (int c = 0; c < kLaneElems / E; ++c) {
-        const uint4 raw = ok ? p[c] : make_uint4(0, 0, 0, 0);
+        const uint4 raw = p[c];
         const typename D::storage* e = reinterpret_cast<const typename D::storage*>(&raw);
 #pragma unroll
         for (int i = 0; i < E; ++i) v[c * E + i] = D::load(e[i]);
@@ -95,8 +117,9 @@ __device__ __forceinline__ void load_lane(const void* src, bool ok, float (&v)[k
 }
 
 // Fused route.  A block holds rows_per_block rows of ngroups 256-groups, one
-// quad per group; quads past the block's rows (or past M) compute on zeros
-// and store nothing, so every lane takes part in the DPP stage and the barrier.
+// quad per group; quads past the block's rows (or past M) compute on row 0
+// and store nothing, so every lane takes part in the DPP stage and the
+// barrier (their group maxima are read by no active lane).
 template <int DT>
 __global__ __launch_bounds__(1024) void convrot_quant_rows(const void* __restrict__ xv,
                                                            int8_t* __restrict__ q,
@@ -114,7 +137,7 @@ __global__ __launch_bounds__(1024) void convrot_quant_rows(const void* __restric
     const int64_t col = static_cast<int64_t>(g) * kRotGroup + d3 * kLaneElems;
 
     float v[kLaneElems];
-    load_lane<DT>(static_cast<const char*>(xv) + ((active ? row : 0) * K + col) * D::bytes, active, v);
+    load_lane<DT>(static_cast<const char*>(xv) + ((active ? row : 0) * K + col) * D::bytes, v);
     lane_stages<kRotGroup>(v);
     float sg[4];
 #pragma unroll
@@ -122,7 +145,7 @@ __global__ __launch_bounds__(1024) void convrot_quant_rows(const void* __restric
     float m = 0.0f;
 #pragma unroll
     for (int r = 0; r < kLaneElems; ++r) {
-        v[r] = h4_across_quad(v[r], sg);
+        v[r] = h4_sum_across_quad(v[r], sg);  // 16 y
         m = fmaxf(m, fabsf(v[r]));
     }
     // quad max: quad_perm [1,0,3,2] then [2,3,0,1]
@@ -135,15 +158,26 @@ __global__ __launch_bounds__(1024) void convrot_quant_rows(const void* __restric
     float amax = 0.0f;
     const float* ga = group_amax + rb * ngroups;
     for (int i = 0; i < ngroups; ++i) amax = fmaxf(amax, ga[i]);
-    const float s = row_scale<DT>(amax, recip != 0);
+    const float s = row_scale<DT>(amax * 0.0625f, recip != 0);
     if (g == 0 && d3 == 0) xs[row] = s;
-    const RowQuant rq = row_quant<DT>(s);
+    // T(y) / T(s) from 16 y: bf16 has fp32's exponent range, so T(16 y) =
+    // 16 T(y) and the divisor becomes 16 T(s) (reciprocal / 16, exact); fp16
+    // (narrow range, absolute denormal steps) rounds y itself.
+    RowQuant rq = row_quant<DT>(s);
+    if constexpr (DT != W8A8_F16) {
+        rq.d *= 16.0f;
+        rq.r *= 0.0625f;
+    }
     uint32_t packed[kLaneElems / 4];
 #pragma unroll
-    for (int j = 0; j < kLaneElems / 4; ++j)
-        packed[j] = pack4_low_bytes(quant_byte<DT>(D::round(v[4 * j]), rq), quant_byte<DT>(D::round(v[4 * j + 1]), rq),
-                                    quant_byte<DT>(D::round(v[4 * j + 2]), rq),
-                                    quant_byte<DT>(D::round(v[4 * j + 3]), rq));
+    for (int j = 0; j < kLaneElems / 4; ++j) {
+        float a[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = (DT == W8A8_F16) ? v[4 * j + i] * 0.0625f : v[4 * j + i];
+        round2<DT>(a[0], a[1]);
+        round2<DT>(a[2], a[3]);
+        packed[j] = quant4_packed<DT>(a[0], a[1], a[2], a[3], rq);
+    }
     uint4* dst = reinterpret_cast<uint4*>(q + row * K + col);
 #pragma unroll
     for (int c = 0; c < kLaneElems / 16; ++c)
@@ -196,7 +230,7 @@ __global__ __launch_bounds__(256) void convrot_rotate_vec(const void* __restrict
     const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const bool ok = c < chunks;
     float v[kLaneElems];
-    load_lane<DT>(static_cast<const char*>(xv) + (ok ? c : 0) * kLaneElems * D::bytes, ok, v);
+    load_lane<DT>(static_cast<const char*>(xv) + (ok ? c : 0) * kLaneElems * D::bytes, v);
     lane_stages<G>(v);
     float sg[4];
 #pragma unroll
@@ -204,11 +238,14 @@ __global__ __launch_bounds__(256) void convrot_rotate_vec(const void* __restrict
     uint4* dst = reinterpret_cast<uint4*>(static_cast<char*>(yv) + (ok ? c : 0) * kLaneElems * D::bytes);
     // G = 256: the quad stage chunk by chunk, each chunk stored as it is done
     // (keeps the live registers to one chunk of stage outputs)
+    // 2^-L, L = log4(G) stages
+    constexpr float kScale = G == 4 ? 0.5f : G == 16 ? 0.25f : G == 64 ? 0.125f : 0.0625f;
 #pragma unroll
     for (int k = 0; k < kLaneElems / E; ++k) {
-        if constexpr (G == kRotGroup) {
 #pragma unroll
-            for (int i = 0; i < E; ++i) v[k * E + i] = h4_across_quad(v[k * E + i], sg);
+        for (int i = 0; i < E; ++i) {
+            if constexpr (G == kRotGroup) v[k * E + i] = h4_sum_across_quad(v[k * E + i], sg);
+            v[k * E + i] *= kScale;
         }
         uint4 out;
         uint32_t* w = reinterpret_cast<uint32_t*>(&out);

@@ -101,15 +101,12 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
             if (c >= nchunks) break;
             if constexpr (E == 8) {
                 uint2 packed;
-                packed.x = pack4_low_bytes(quant_byte<DT>(elem(r, j, 0), rq), quant_byte<DT>(elem(r, j, 1), rq),
-                                           quant_byte<DT>(elem(r, j, 2), rq), quant_byte<DT>(elem(r, j, 3), rq));
-                packed.y = pack4_low_bytes(quant_byte<DT>(elem(r, j, 4), rq), quant_byte<DT>(elem(r, j, 5), rq),
-                                           quant_byte<DT>(elem(r, j, 6), rq), quant_byte<DT>(elem(r, j, 7), rq));
+                packed.x = quant4_packed<DT>(elem(r, j, 0), elem(r, j, 1), elem(r, j, 2), elem(r, j, 3), rq);
+                packed.y = quant4_packed<DT>(elem(r, j, 4), elem(r, j, 5), elem(r, j, 6), elem(r, j, 7), rq);
                 *reinterpret_cast<uint2*>(dst + c * E) = packed;
             } else {
                 *reinterpret_cast<uint32_t*>(dst + c * E) =
-                    pack4_low_bytes(quant_byte<DT>(elem(r, j, 0), rq), quant_byte<DT>(elem(r, j, 1), rq),
-                                    quant_byte<DT>(elem(r, j, 2), rq), quant_byte<DT>(elem(r, j, 3), rq));
+                    quant4_packed<DT>(elem(r, j, 0), elem(r, j, 1), elem(r, j, 2), elem(r, j, 3), rq);
             }
         }
     }

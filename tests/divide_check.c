@@ -1,17 +1,20 @@
 /* Exhaustive check of the quantizer's division (used by tests/test_divide.py).
  *
- * The HIP quantizer computes RN(x / d) for a 16-bit input x and the row's
- * divisor d = T(s) as  q0 = RN(x * r), e = RN(fma(-q0, d, x)), q = RN(fma(e, r, q0))
- * with r = RN(1 / d)  (imagine_amd/csrc/w8a8_common.h, div_rn).  This program
- * compares that with the IEEE quotient for every pair the quantizer can see:
+ * The HIP quantizers form the int8 code of a 16-bit input x and the row's
+ * divisor d = T(s) from q0 = RN(x * r), r = RN(1 / d)
+ * (imagine_amd/csrc/w8a8_common.h, code_quotient).  This program compares
+ * that, and the one-fma-corrected quotient q = RN(fma(RN(fma(-q0, d, x)), r, q0)),
+ * with the IEEE quotient for every pair the quantizer can see:
  * every reachable 16-bit divisor d and every finite 16-bit x with
  * |x| <= 128 * d (a row's elements never exceed amax, and d >= amax/127 up to
  * one 16-bit rounding).  Sign symmetry covers negative x.  Requirements: the
  * final int8 code clamp(rint(T(q))) equals the IEEE one for every pair, and
  * the fp32 quotient itself is identical whenever x and x/d are >= 2^-100 (else the
  * fma remainder or the quotient is subnormal and loses bits; the quotient
- * is then below 2^-70 and both codes are 0).  Prints mismatch counts; exit 0
- * iff none.
+ * is then below 2^-70 and both codes are 0).  Also required: the code from the
+ * uncorrected product q0 = RN(x * r) alone equals the IEEE code for every pair
+ * (the kernels that only need the int8 code use q0).  Prints mismatch counts;
+ * exit 0 iff none.
  * Usage: divide_check bf16|f16
  */
 #include <math.h>
@@ -59,7 +62,7 @@ static int code(float q, int bf) {
 
 int main(int argc, char** argv) {
     int bf = argc > 1 && strcmp(argv[1], "bf16") == 0;
-    long long pairs = 0, bad_code = 0, bad_quot = 0;
+    long long pairs = 0, bad_code = 0, bad_quot = 0, bad_prod = 0;
     for (uint32_t dh = 1; dh < 0x7f80u; ++dh) {
         float d = bf ? bf16_val((uint16_t)dh) : f16_val((uint16_t)dh);
         if (!bf && dh >= 0x7c00u) break; /* f16 inf/nan */
@@ -82,13 +85,17 @@ int main(int argc, char** argv) {
                 if (bad_code < 10) printf("code mismatch d=%a x=%a got=%a want=%a\n", d, x, q, ref);
                 ++bad_code;
             }
+            if (code(q0, bf) != code(ref, bf)) {
+                if (bad_prod < 10) printf("product code mismatch d=%a x=%a got=%a want=%a\n", d, x, q0, ref);
+                ++bad_prod;
+            }
             if (x >= 0x1p-100f && ref >= 0x1p-100f && f2u(q) != f2u(ref)) {
                 if (bad_quot < 10) printf("quotient mismatch d=%a x=%a got=%a want=%a\n", d, x, q, ref);
                 ++bad_quot;
             }
         }
     }
-    printf("%s pairs=%lld code_mismatches=%lld quotient_mismatches=%lld\n",
-           bf ? "bf16" : "f16", pairs, bad_code, bad_quot);
-    return (bad_code != 0 || bad_quot != 0);
+    printf("%s pairs=%lld code_mismatches=%lld quotient_mismatches=%lld product_code_mismatches=%lld\n",
+           bf ? "bf16" : "f16", pairs, bad_code, bad_quot, bad_prod);
+    return (bad_code != 0 || bad_quot != 0 || bad_prod != 0);
 }
