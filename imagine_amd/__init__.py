@@ -6,9 +6,11 @@ Drop-in for the reference crate's ``int8_linear`` operator
 """
 from . import _lib
 from .ops import (apply_residual, convrot_rotate, dequantize_linear, gemm_dequant, gemm_dequant_residual,
-                  gemm_dequant_xq, gemm_i32, gemv_dequant, gemv_dequant_residual, int8_linear, quantize_rowwise,
-                  quantize_rowwise_convrot, route, row_scales)
+                  gemm_dequant_xq, gemm_i32, gemv_dequant, gemv_dequant_residual, int8_linear,
+                  quantize_convrot_weight, quantize_rowwise, quantize_rowwise_convrot, quantize_tensorwise, route,
+                  row_scales)
 
 __all__ = ["int8_linear", "quantize_rowwise", "row_scales", "gemv_dequant", "gemv_dequant_residual",
            "gemm_dequant", "gemm_dequant_residual", "gemm_dequant_xq", "gemm_i32", "dequantize_linear",
-           "apply_residual", "convrot_rotate", "quantize_rowwise_convrot", "route", "_lib"]
+           "apply_residual", "convrot_rotate", "quantize_rowwise_convrot", "quantize_tensorwise",
+           "quantize_convrot_weight", "route", "_lib"]

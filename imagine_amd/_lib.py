@@ -15,6 +15,7 @@ ACT_GELU_TANH = 1 << 1
 OUT_INT32 = 1 << 2
 FUSED_QUANT = 1 << 3
 ROUTE_GEMM = 1 << 4
+GIVEN_SCALE = 1 << 5
 
 # Every symbol include/w8a8.h declares, with (restype, argtypes).
 _p, _i, _i64, _u32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32
@@ -43,6 +44,9 @@ SIGNATURES = {
     "w8a8_int8_linear_convrot_workspace_bytes": (_i64, [_i64, _i64, _i64, _i]),
     "w8a8_int8_linear_convrot": (_i, [_p, _i, _p, _p, _i64, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _i64,
                                       _u32, _p, _i64, _p]),
+    "w8a8_quantize_tensorwise": (_i, [_p, _i, _p, _p, _i64, _u32, _p]),
+    "w8a8_convrot_weight_workspace_bytes": (_i64, [_i64, _i64, _i64, _i]),
+    "w8a8_quantize_convrot_weight": (_i, [_p, _i, _p, _p, _i64, _i64, _i64, _u32, _p, _i64, _p]),
 }
 
 _lib = None

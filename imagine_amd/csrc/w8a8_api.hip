@@ -32,6 +32,9 @@ void launch_convrot_quant(const void* x, int x_dtype, int8_t* q, float* xs, int6
                           bool recip, hipStream_t stream);
 void launch_convrot_rotate(const void* x, int x_dtype, void* y, int64_t M, int64_t K, int64_t G,
                            hipStream_t stream);
+bool convrot_weight_fused(const void* w, const void* q, int64_t K, int64_t group);
+void launch_quantize_tensorwise(const void* x, int x_dtype, int8_t* q, float* scale, int64_t n, bool given,
+                                bool recip, hipStream_t stream);
 }  // namespace w8a8
 
 namespace {
@@ -56,7 +59,7 @@ int check_launch(const char* what) {
 bool valid_dtype(int d) { return d == W8A8_F32 || d == W8A8_F16 || d == W8A8_BF16; }
 
 constexpr uint32_t kKnownFlags = W8A8_SCALE_RECIP | W8A8_ACT_GELU_TANH | W8A8_OUT_INT32 |
-                                 W8A8_FUSED_QUANT | W8A8_ROUTE_GEMM;
+                                 W8A8_FUSED_QUANT | W8A8_ROUTE_GEMM | W8A8_GIVEN_SCALE;
 
 int check_common(int64_t M, int64_t N, int64_t K, uint32_t flags) {
     if (M < 0 || N < 0 || K < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
@@ -271,6 +274,51 @@ int w8a8_quantize_rowwise_convrot(const void* x, int x_dtype, int8_t* q, float* 
         return fail(W8A8_ERR_VALUE, "rotated buffer smaller than w8a8_convrot_workspace_bytes(M, K, group, dtype)");
     if (int rc = w8a8_convrot_rotate(x, x_dtype, rotated, M, K, group, stream)) return rc;
     return w8a8_quantize_rowwise(rotated, x_dtype, q, xs, M, K, flags, stream);
+}
+
+int w8a8_quantize_tensorwise(const void* x, int x_dtype, int8_t* q, float* scale, int64_t n, uint32_t flags,
+                             hipStream_t stream) {
+    if (n < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (flags & ~(W8A8_SCALE_RECIP | W8A8_GIVEN_SCALE))
+        return fail(W8A8_ERR_VALUE, "the tensorwise quantizer takes W8A8_SCALE_RECIP and W8A8_GIVEN_SCALE");
+    if (!valid_dtype(x_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for INT8 quantization");
+    if (!scale) return fail(W8A8_ERR_VALUE, "null scale pointer");
+    if (n > 0 && (!x || !q)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    w8a8::launch_quantize_tensorwise(x, x_dtype, q, scale, n, flags & W8A8_GIVEN_SCALE, flags & W8A8_SCALE_RECIP,
+                                     stream);
+    return check_launch("quantize_int8_tensorwise");
+}
+
+int64_t w8a8_convrot_weight_workspace_bytes(int64_t N, int64_t K, int64_t group, int w_dtype) {
+    if (N < 0 || K < 0 || !valid_dtype(w_dtype)) return -1;
+    if (group == 256 && K % 256 == 0 && K <= 65536) return 0;
+    return N * K * (w_dtype == W8A8_F32 ? 4 : 2);
+}
+
+int w8a8_quantize_convrot_weight(const void* w, int w_dtype, int8_t* q, float* scale, int64_t N, int64_t K,
+                                 int64_t group, uint32_t flags, void* rotated, int64_t rotated_bytes,
+                                 hipStream_t stream) {
+    if (int rc = check_common(N, 0, K, flags)) return rc;
+    if (flags & ~W8A8_SCALE_RECIP)
+        return fail(W8A8_ERR_VALUE, "the ConvRot quantizer takes only W8A8_SCALE_RECIP");
+    if (int rc = check_convrot_group(K, group)) return rc;
+    if (!valid_dtype(w_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for INT8 quantization");
+    if (N == 0) return W8A8_OK;
+    if (K > 0 && (!w || !q)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (!scale) return fail(W8A8_ERR_VALUE, "null scale pointer");
+    const bool recip = flags & W8A8_SCALE_RECIP;
+    if (K == 0) return w8a8_quantize_rowwise(w, w_dtype, q, scale, N, K, flags, stream);
+    if (w8a8_convrot_weight_workspace_bytes(N, K, group, w_dtype) == 0) {
+        if (!w8a8::convrot_weight_fused(w, q, K, group))
+            return fail(W8A8_ERR_RUNTIME, "ConvRot weight and code rows above K = 16384 must be 16-byte aligned");
+        w8a8::launch_convrot_quant(w, w_dtype, q, scale, N, K, recip, stream);
+        return check_launch("quantize_int8_convrot_weight");
+    }
+    if (!rotated || rotated_bytes < w8a8_convrot_weight_workspace_bytes(N, K, group, w_dtype))
+        return fail(W8A8_ERR_VALUE,
+                    "rotated buffer smaller than w8a8_convrot_weight_workspace_bytes(N, K, group, dtype)");
+    if (int rc = w8a8_convrot_rotate(w, w_dtype, rotated, N, K, group, stream)) return rc;
+    return w8a8_quantize_rowwise(rotated, w_dtype, q, scale, N, K, flags, stream);
 }
 
 int64_t w8a8_int8_linear_convrot_workspace_bytes(int64_t M, int64_t K, int64_t group, int x_dtype) {

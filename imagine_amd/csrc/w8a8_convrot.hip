@@ -288,6 +288,14 @@ bool convrot_fused_route(int64_t K, int64_t group) {
     return group == kRotGroup && K % kRotGroup == 0 && K >= kRotGroup && K <= 16384;
 }
 
+// Weights take the fused numerics up to K = 65536 (a block of 1024 threads
+// holds one row); rows above K = 16384 need the aligned (register) kernel,
+// i.e. 16-byte aligned weight and code rows.
+bool convrot_weight_fused(const void* w, const void* q, int64_t K, int64_t group) {
+    if (group != kRotGroup || K % kRotGroup != 0 || K < kRotGroup || K > 65536) return false;
+    return K <= 16384 || (reinterpret_cast<uintptr_t>(w) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0);
+}
+
 // Rows per block of the fused kernel: whole waves with every quad busy where
 // possible (ngroups * rows % 16 == 0), about 256 threads, at most 1024.
 static int fused_rows_per_block(int ngroups) {

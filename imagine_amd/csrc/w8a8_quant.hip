@@ -11,6 +11,8 @@
 // issues 128-bit loads, the absmax is a wave64 butterfly (plus a 4-entry LDS
 // exchange for 4-wave rows), and the int8 codes leave as 64-bit stores.
 // Rows that do not fit, or unaligned operands, take the generic kernel.
+#include <algorithm>
+
 #include "w8a8_common.h"
 
 namespace w8a8 {
@@ -182,6 +184,110 @@ static void quant_dispatch_dt(const void* x, int8_t* q, float* xs, int64_t M, in
     if (aligned && dispatch_vec<DT, GELU, SO>(x, q, xs, M, K, recip, stream)) return;
     hipLaunchKernelGGL((quant_rows_generic<DT, GELU, SO>), dim3(static_cast<unsigned>(M)),
                        dim3(256), 0, stream, x, q, xs, M, K, recip);
+}
+
+// ---------------------------------------------------------------- tensorwise
+
+// Tensorwise quantization: one scale for the whole tensor (the reference's
+// quantize_int8_tensorwise, inference/src/eager.rs:134-151).  Three kernels
+// on one stream: the absolute maximum into the scale slot (an atomic max of
+// the bits of non-negative floats, which order like the floats), the codes
+// from it, then the scale written over it once every block has read it.
+
+__global__ void tensor_amax_clear(float* acc) {
+    if (threadIdx.x == 0) acc[0] = 0.0f;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void tensor_amax(const void* __restrict__ xv, int64_t n, bool vec,
+                                                   unsigned* __restrict__ acc_bits) {
+    using D = DType<DT>;
+    constexpr int E = 16 / D::bytes;
+    __shared__ float part[4];
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    float m = 0.0f;
+    if (vec) {
+        const uint4* x = static_cast<const uint4*>(xv);
+        for (int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < n / E; c += stride) {
+            const uint4 raw = x[c];
+            const typename D::storage* e = reinterpret_cast<const typename D::storage*>(&raw);
+#pragma unroll
+            for (int i = 0; i < E; ++i) m = fmaxf(m, fabsf(D::load(e[i])));
+        }
+    } else {
+        const typename D::storage* x = static_cast<const typename D::storage*>(xv);
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+            m = fmaxf(m, fabsf(D::load(x[i])));
+    }
+    m = wave_max(m);
+    if ((threadIdx.x % kWave) == 0) part[threadIdx.x / kWave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+        atomicMax(acc_bits, __float_as_uint(m));
+    }
+}
+
+// scale_src holds the given scale (given) or the maximum (else).
+template <int DT>
+__global__ __launch_bounds__(256) void tensor_quant(const void* __restrict__ xv, int8_t* __restrict__ q,
+                                                    int64_t n, bool vec, const float* __restrict__ scale_src,
+                                                    bool given, int recip) {
+    using D = DType<DT>;
+    constexpr int E = 16 / D::bytes;
+    const float s = given ? scale_src[0] : row_scale<DT>(scale_src[0], recip != 0);
+    const RowQuant rq = row_quant<DT>(s);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    if (vec) {
+        const uint4* x = static_cast<const uint4*>(xv);
+        for (int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < n / E; c += stride) {
+            const uint4 raw = x[c];
+            const typename D::storage* e = reinterpret_cast<const typename D::storage*>(&raw);
+            if constexpr (E == 8) {
+                uint2 packed;
+                packed.x = quant4_packed<DT>(D::load(e[0]), D::load(e[1]), D::load(e[2]), D::load(e[3]), rq);
+                packed.y = quant4_packed<DT>(D::load(e[4]), D::load(e[5]), D::load(e[6]), D::load(e[7]), rq);
+                reinterpret_cast<uint2*>(q)[c] = packed;
+            } else {
+                reinterpret_cast<uint32_t*>(q)[c] =
+                    quant4_packed<DT>(D::load(e[0]), D::load(e[1]), D::load(e[2]), D::load(e[3]), rq);
+            }
+        }
+    } else {
+        const typename D::storage* x = static_cast<const typename D::storage*>(xv);
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+            q[i] = static_cast<int8_t>(quant_elem<DT>(D::load(x[i]), rq));
+    }
+}
+
+template <int DT>
+__global__ void tensor_scale_store(float* scale, int recip) {
+    if (threadIdx.x == 0) scale[0] = row_scale<DT>(scale[0], recip != 0);
+}
+
+template <int DT>
+static void tensorwise_dt(const void* x, int8_t* q, float* scale, int64_t n, bool given, bool recip,
+                          hipStream_t stream) {
+    constexpr int E = 16 / DType<DT>::bytes;
+    const bool vec = n % E == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(q) % E == 0;
+    const int64_t work = vec ? n / E : n;
+    const dim3 grid(static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>((work + 255) / 256, 4096))));
+    if (!given) {
+        hipLaunchKernelGGL(tensor_amax_clear, dim3(1), dim3(64), 0, stream, scale);
+        hipLaunchKernelGGL((tensor_amax<DT>), grid, dim3(256), 0, stream, x, n, vec,
+                           reinterpret_cast<unsigned*>(scale));
+    }
+    hipLaunchKernelGGL((tensor_quant<DT>), grid, dim3(256), 0, stream, x, q, n, vec, scale, given,
+                       recip ? 1 : 0);
+    if (!given) hipLaunchKernelGGL((tensor_scale_store<DT>), dim3(1), dim3(64), 0, stream, scale, recip ? 1 : 0);
+}
+
+void launch_quantize_tensorwise(const void* x, int x_dtype, int8_t* q, float* scale, int64_t n, bool given,
+                                bool recip, hipStream_t stream) {
+    if (x_dtype == W8A8_BF16) tensorwise_dt<W8A8_BF16>(x, q, scale, n, given, recip, stream);
+    else if (x_dtype == W8A8_F16) tensorwise_dt<W8A8_F16>(x, q, scale, n, given, recip, stream);
+    else tensorwise_dt<W8A8_F32>(x, q, scale, n, given, recip, stream);
 }
 
 // Host entry used by the C ABI: x_dtype is a W8A8_* code (validated by the caller).

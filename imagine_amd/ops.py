@@ -123,6 +123,45 @@ def quantize_rowwise_convrot(x, group=256, scale_form="ieee"):
     return q, s
 
 
+def quantize_tensorwise(x, scale=None, scale_form="ieee"):
+    """One scale for the whole tensor -> (q int8 of x's shape, s fp32 scalar):
+    the reference's quantize_int8_tensorwise (inference/src/eager.rs:134-151).
+    ``scale`` (a number or a one-element tensor) replaces the computed scale and
+    is returned as given (an fp32 device tensor)."""
+    _require_cuda(x)
+    xc = x.contiguous()
+    q = torch.empty(xc.shape, dtype=torch.int8, device=x.device)
+    flags = _lib.SCALE_RECIP if scale_form == "recip" else 0
+    if scale is None:
+        s = torch.empty((), dtype=torch.float32, device=x.device)
+    else:
+        s = torch.as_tensor(scale).to(device=x.device, dtype=torch.float32).reshape(())  # read, not written
+        flags |= _lib.GIVEN_SCALE
+    _lib.check(_lib.load().w8a8_quantize_tensorwise(_ptr(xc), _dtype_code(xc.dtype, "INT8 quantization"), _ptr(q),
+                                                    _ptr(s), xc.numel(), flags, _stream(x.device)))
+    return q, s
+
+
+def quantize_convrot_weight(w, group=256, scale_form="ieee"):
+    """ConvRot weight quantization [N, K] -> (q int8 [N, K], s fp32 [N, 1]): the
+    reference's quantize_int8_convrot_weight (inference/src/convrot.rs:378-429)."""
+    _require_cuda(w)
+    if w.dim() != 2:
+        raise ValueError("ConvRot INT8 weight quantization expects a 2D weight tensor")
+    w = w.contiguous()
+    N, K = w.shape
+    code = _dtype_code(w.dtype, "INT8 quantization")
+    q = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    s = torch.empty((N, 1), dtype=torch.float32, device=w.device)
+    lib = _lib.load()
+    rot_bytes = lib.w8a8_convrot_weight_workspace_bytes(N, K, group, code)
+    rotated = torch.empty(rot_bytes, dtype=torch.uint8, device=w.device) if rot_bytes > 0 else None
+    flags = _lib.SCALE_RECIP if scale_form == "recip" else 0
+    _lib.check(lib.w8a8_quantize_convrot_weight(_ptr(w), code, _ptr(q), _ptr(s), N, K, group, flags,
+                                                _ptr(rotated), max(rot_bytes, 0), _stream(w.device)))
+    return q, s
+
+
 def row_scales(x, scale_form="ieee"):
     """Row scales only (fp32 [M, 1]); the first pass of the fused quant+GEMM."""
     _require_cuda(x)

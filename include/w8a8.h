@@ -56,6 +56,8 @@ extern "C" {
 #define W8A8_FUSED_QUANT (1u << 3)   /* w8a8_int8_linear: GEMM route quantizes x inside
                                         the GEMM's activation-tile load */
 #define W8A8_ROUTE_GEMM (1u << 4)    /* w8a8_int8_linear: skip the M<=2 GEMV routes */
+#define W8A8_GIVEN_SCALE (1u << 5)   /* w8a8_quantize_tensorwise: *scale holds the scale
+                                        to quantize with (the reference's scale argument) */
 
 const char* w8a8_last_error(void);
 int w8a8_last_accelerator_code(void);
@@ -199,6 +201,33 @@ int w8a8_int8_linear_convrot(const void* x, int x_dtype, const int8_t* w, const 
                              int64_t rscale_size, const void* resid, void* out, int out_dtype,
                              int64_t M, int64_t N, int64_t K, int64_t group, uint32_t flags,
                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* ---- Weight quantizers (TensorWiseINT8Layout.from_float) -----------------
+ * The layout's quantize step (inference/src/layout_complete.rs:119-160):
+ * per-channel weights use w8a8_quantize_rowwise over the N rows, tensorwise
+ * weights w8a8_quantize_tensorwise, ConvRot weights
+ * w8a8_quantize_convrot_weight. */
+
+/* One scale for all n elements of x (quantize_int8_tensorwise,
+ * inference/src/eager.rs:134-151, which the reference's CUDA backend runs too,
+ * backend_bindings.rs:549-585): s = max(amax / 127, 1e-30), or the caller's
+ * scale with W8A8_GIVEN_SCALE; q = clamp(rint(T(x / T(s)))).  scale is one
+ * fp32 in device memory (written unless W8A8_GIVEN_SCALE).  Flags:
+ * W8A8_SCALE_RECIP, W8A8_GIVEN_SCALE. */
+int w8a8_quantize_tensorwise(const void* x, int x_dtype, int8_t* q, float* scale, int64_t n,
+                             uint32_t flags, hipStream_t stream);
+
+/* ConvRot weight quantization w [N, K] -> q [N, K], per-row scales [N]
+ * (quantize_int8_convrot_weight, inference/src/convrot.rs:378-429; path choice
+ * weight_path :345-372): group 256 with K % 256 == 0 (up to K = 65536) takes
+ * the fused rotation's numerics (fp32 rotated values, absmax over them),
+ * like the reference's Rowwise64 and Staged paths; other groups rotate
+ * (rounded to the dtype) and quantize rowwise, like its EagerRotation path,
+ * using `rotated` (w8a8_convrot_weight_workspace_bytes).  Flags: W8A8_SCALE_RECIP. */
+int64_t w8a8_convrot_weight_workspace_bytes(int64_t N, int64_t K, int64_t group, int w_dtype);
+int w8a8_quantize_convrot_weight(const void* w, int w_dtype, int8_t* q, float* scale, int64_t N,
+                                 int64_t K, int64_t group, uint32_t flags, void* rotated,
+                                 int64_t rotated_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,7 @@ def lib():
         f.w8o_gemm_i32.argtypes = [p, p, i64, i64, i64, p]
         f.w8o_epilogue_kitchen.argtypes = [p, p, p, i64, p, p, i32, i64, i64, i32, i32]
         f.w8o_residual.argtypes = [p, p, p, i64, i32, i64, i64, i32]
+        f.w8o_quant_tensorwise.argtypes = [p, i32, i64, p, i32, p, p]
         f.w8o_convrot_rotate.argtypes = [p, i32, i64, i64, i64, p, p]
         f.w8o_convrot_quant.argtypes = [p, i32, i64, i64, i64, i32, p, p, p]
         f.w8o_epilogue_eager.argtypes = [p, p, p, i64, p, p, i32, i64, i64]
@@ -96,6 +97,18 @@ def quant_rowwise(x, dtype, scale_mode=0, act=0):
     return q, s
 
 
+def quant_tensorwise(x, dtype, scale=None, scale_mode=0):
+    """Tensorwise quantization of ``x`` (any shape) -> (q int8, s fp32 scalar);
+    ``scale`` (a float) replaces the computed scale."""
+    x = np.ascontiguousarray(x, dtype=_storage(dtype))
+    q = np.empty(x.shape, np.int8)
+    s = np.empty((1,), np.float32)
+    given = None if scale is None else np.array([scale], np.float32)
+    lib().w8o_quant_tensorwise(_ptr(x), DTYPE_CODE[dtype], x.size, None if given is None else _ptr(given),
+                               scale_mode, _ptr(q), _ptr(s))
+    return q, s[0]
+
+
 def convrot_fused_route(k, group):
     """The reference's fused-rotation predicate (cuda_linear.rs:404-417):
     group 256, K a multiple of 256 in [256, 16384]."""
@@ -126,6 +139,22 @@ def convrot_quant(x, dtype, group, scale_mode=0):
     work = np.empty((K,), np.float32)
     lib().w8o_convrot_quant(_ptr(x), DTYPE_CODE[dtype], M, K, group, scale_mode, _ptr(q), _ptr(s),
                             _ptr(work))
+    return q, s
+
+
+def convrot_quant_weight(w, dtype, group, scale_mode=0):
+    """ConvRot weight quantization [N, K] by the reference's weight path
+    (inference/src/convrot.rs:345-372): group 256 with K % 256 == 0 takes the
+    fused numerics at any K (its Rowwise64 and Staged paths), other groups
+    rotate then quantize rowwise (EagerRotation)."""
+    w = np.ascontiguousarray(w, dtype=_storage(dtype))
+    N, K = w.shape
+    if not (group == 256 and K % 256 == 0):
+        return quant_rowwise(convrot_rotate(w, dtype, group), dtype, scale_mode=scale_mode)
+    q = np.empty((N, K), np.int8)
+    s = np.empty((N,), np.float32)
+    work = np.empty((K,), np.float32)
+    lib().w8o_convrot_quant(_ptr(w), DTYPE_CODE[dtype], N, K, group, scale_mode, _ptr(q), _ptr(s), _ptr(work))
     return q, s
 
 

@@ -26,6 +26,8 @@
  *   w8o_gelu_tanh        reference gelu_tanh activation payloads (1 bf16 ulp).
  *   w8o_residual         reference CUDA residual payloads (fused, unaligned and
  *                        eager residual modes of the GEMM, GEMV and M=1 routes).
+ *   w8o_quant_tensorwise reference tensorwise golden vectors
+ *                        (reference_primitives.py:357-365, deterministic cases).
  *   w8o_convrot_*        reference ConvRot CUDA payloads (fused group-256 route
  *                        and rotate-then-quantize route); the stage order against
  *                        a dense float64 Hadamard matmul (H built by Kronecker
@@ -196,6 +198,31 @@ void w8o_quant_rowwise(const void* x, int dtype, int64_t M, int64_t K, int scale
             q[m * K + k] = quant_value(v, sT, dtype);
         }
     }
+}
+
+/* Tensorwise INT8 quantization (inference/src/eager.rs:134-151; the CUDA
+ * backend runs the same eager body, backend_bindings.rs:549-585):
+ *   s = given ? *given : max(float(amax |x|) / 127, 1e-30)   (scale_mode 1:
+ *       the amax * (1/127) form of w8o_quant_rowwise)
+ *   q = int8(clamp(round_half_even(dtype(float(x) / float(sT))), -128, 127)),
+ *       sT = dtype(s), a zero sT replaced by tiny(dtype).
+ * x has n elements; *s receives the scale. */
+void w8o_quant_tensorwise(const void* x, int dtype, int64_t n, const float* given, int scale_mode,
+                          int8_t* q, float* s) {
+    float scale;
+    if (given) {
+        scale = *given;
+    } else {
+        float amax = 0.0f;
+        for (int64_t i = 0; i < n; ++i) {
+            float a = fabsf(load_as_f32(x, dtype, i));
+            if (a > amax) amax = a;
+        }
+        scale = row_scale(amax, dtype, scale_mode);
+    }
+    *s = scale;
+    const float sT = scale_in_dtype(scale, dtype);
+    for (int64_t i = 0; i < n; ++i) q[i] = quant_value(load_as_f32(x, dtype, i), sT, dtype);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -77,6 +77,8 @@ def main():
         "cuda_int8_m1": committed["sections"]["cuda_int8_m1"],
         "cuda_int8_m1_selection": committed["sections"]["cuda_int8_m1_selection"],
         "int8_rowwise": [c for c in archived["int8"] if c["rowwise"]],
+        # tensorwise quantizer, deterministic rounding only (seed None or 0)
+        "int8_tensorwise": [c for c in archived["int8"] if not c["rowwise"] and not c["seed"]],
         "native_int8_rowwise": [c for c in archived["native_quantizers"]
                                 if c.get("operation") == "int8_rowwise"],
         "int8_mm": archived["int8_mm"],
@@ -84,7 +86,7 @@ def main():
         "cuda_int8_gemv": archived["cuda_int8_gemv"],
         "cuda_int8_gemm": archived["cuda_int8_gemm"],
     }
-    for c in fixtures["int8_rowwise"]:
+    for c in fixtures["int8_rowwise"] + fixtures["int8_tensorwise"]:
         c.pop("decoded", None)
     raw = json.dumps(fixtures, separators=(",", ":")).encode()
     with gzip.GzipFile(OUT, "wb", mtime=0) as f:

@@ -73,6 +73,22 @@ def test_quant_matches_reference_rowwise_golden_vectors():
     assert n == 6
 
 
+def test_tensorwise_quant_matches_reference_golden_vectors():
+    """reference_primitives.py:357-365: eager tensorwise quant (CPU and CUDA
+    devices) with a recalculated, a zero and an explicit scale; a zero scale
+    divides by the dtype's tiny, saturating every nonzero code."""
+    n = 0
+    for c in FX.load()["int8_tensorwise"]:
+        xd = OP.dtype_name(c["dtype"])
+        x = O.to_dtype(OP.quantizer_x_primitives(), xd)
+        given = {"recalculate": None, "zero": 0.0, "explicit": 0.03125}[c["scale_mode"]]
+        q, s = O.quant_tensorwise(x, xd, scale=given, scale_mode=0)
+        assert q.view(np.uint8).reshape(-1).tolist() == c["payload"], c
+        assert np.array([s], np.float32).view(np.uint8).tolist() == c["scale"], c
+        n += 1
+    assert n == 36
+
+
 def test_quant_matches_reference_cuda_kernel_golden_vectors():
     """reference_primitives.py:388-391: Kitchen's quantize_int8_rowwise kernel."""
     cases = [c for c in FX.load()["native_int8_rowwise"] if c["seed"] is None]
