@@ -43,7 +43,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--only", default=None,
                    help="run only one kernel in a loop (for rocprofv3 counters): "
-                        "up_gemm | quant | step | copy")
+                        "up_gemm | quant | convrot_quant | step | copy")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     return p.parse_args()
@@ -292,6 +292,16 @@ def measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv):
         ex[f"quant_K{k}"] = {"us": round(ms * 1e3, 2), "GB/s": round(per / (ms * 1e-3) / 1e9, 1),
                              "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
                              "bytes": per, "buffer_sets": nsets}
+
+        # ConvRot (Hadamard-256 rotation fused into the quantizer), same bytes
+        def run_convrot(i):
+            j = i % nsets
+            W._lib.check(lib.w8a8_quantize_rowwise_convrot(xs[j].data_ptr(), W._lib.BF16, qs[j].data_ptr(),
+                                                           ss.data_ptr(), M_TOK, k, 256, 0, None, 0, stream()))
+        ms = median_of_batches(run_convrot)
+        ex[f"convrot_quant_K{k}"] = {"us": round(ms * 1e3, 2), "GB/s": round(per / (ms * 1e-3) / 1e9, 1),
+                                     "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+                                     "bytes": per, "buffer_sets": nsets}
         del xs, qs
     # adaLN GEMV, M=2 K=3072 N=18432, rotating weights
     m, k, n = 2, 3072, 18432
@@ -347,6 +357,12 @@ def run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs):
     elif args.only == "quant":
         for _ in range(n_iter):
             quant(x_ffn, qbuf[HID])
+    elif args.only == "convrot_quant":
+        s = torch.empty(M_TOK, dtype=torch.float32, device=dev)
+        for _ in range(n_iter):
+            W._lib.check(lib.w8a8_quantize_rowwise_convrot(x_ffn.data_ptr(), W._lib.BF16, qbuf[HID].data_ptr(),
+                                                           s.data_ptr(), M_TOK, HID, 256, 0, None, 0,
+                                                           torch.cuda.current_stream().cuda_stream))
     elif args.only == "step":
         for _ in range(n_iter):
             step()
