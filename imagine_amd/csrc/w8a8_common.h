@@ -121,24 +121,39 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // GELU-tanh of an epilogue output (rounded to a 16-bit output afterwards,
 // where one ulp of slack is allowed), in the reference's structure
 // 0.5 x (1 + tanh(u)) but with fewer operations than gelu_tanh:
-//   u = x (beta + beta kappa x^2)           (one fma; the reference's order
-//                                            rounds u differently by ~1 ulp)
-//   t = exp(-2|u|),  r = 1 - 2t / (1 + t)   (|tanh u|; the subtraction rounds
-//                                            like the reference's fp32 tanh, so
-//                                            1 + tanh(u) cancels as it does:
-//                                            exactly 0 once |u| > 9)
-//   gelu = (0.5 x) (1 + copysign(r, u))
+//   e = x (a + b x^2) = 2u / ln 2           (sqrt(2/pi) and 0.044715 pre-scaled
+//                                            by 2 / ln 2, so exp2 takes -|e|
+//                                            through its input modifiers; u
+//                                            has the sign of x)
+//   t = exp(-2|u|),  r = 1 - 2 t / (1 + t)  (|tanh u| as one fma; the
+//                                            subtraction rounds like the
+//                                            reference's fp32 tanh, so 1 + tanh u
+//                                            cancels as it does: exactly 0 once
+//                                            |u| > 9)
+//   gelu = (x/2) (1 + copysign(r, x))       (the reference's two roundings:
+//                                            a single fma would turn the -0 of
+//                                            the saturated negative tail into
+//                                            +0)
 // Near u = 0 r carries an absolute error of ~2^-24, which only moves the
 // 1 + tanh(u) term by an ulp.  The quantizer's input activation, whose int8
 // codes are compared bit for bit, keeps gelu_tanh.
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
-    const float kBeta = 0.79788456080286535588f;        // sqrt(2/pi)
-    const float kBetaKappa = 0.035677408136300125f;      // sqrt(2/pi) * 0.044715
-    const float kMinus2Log2e = -2.88539008177792681472f; // -2 / ln(2)
-    const float u = x * fmaf(kBetaKappa, x * x, kBeta);
-    const float t = __builtin_amdgcn_exp2f(fabsf(u) * kMinus2Log2e);   // (0, 1]
-    const float r = 1.0f - (t + t) * __builtin_amdgcn_rcpf(1.0f + t);
-    return (0.5f * x) * (1.0f + __builtin_copysignf(r, u));
+    const float kA = 2.302208198144325f;      // sqrt(2/pi) * 2 / ln 2
+    const float kB = 0.1029432395800235f;     // sqrt(2/pi) * 0.044715 * 2 / ln 2
+    const float e = x * fmaf(kB, x * x, kA);
+    const float t = __builtin_amdgcn_exp2f(-fabsf(e));   // (0, 1]
+    const float q = t * __builtin_amdgcn_rcpf(1.0f + t);
+    const float r = fmaf(-2.0f, q, 1.0f);
+    return (0.5f * x) * (1.0f + __builtin_copysignf(r, x));
+}
+
+// Two bf16 pre-activations packed in one word (low half first) -> their
+// GELU-tanh, packed the same way.  Equal to rounding each input with
+// DType<bf16>::round and applying gelu_tanh_fast, with the pair rounded by one
+// v_cvt_pk_bf16_f32 on each side.
+__device__ __forceinline__ uint32_t gelu_bf16x2(uint32_t p) {
+    return pack2_bf16(gelu_tanh_fast(__uint_as_float(p << 16)),
+                      gelu_tanh_fast(__uint_as_float(p & 0xffff0000u)));
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used

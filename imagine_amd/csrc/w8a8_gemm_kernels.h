@@ -399,6 +399,27 @@ struct DmaCfg {
     static constexpr int kLds = STAGES * kTileBytes;
     // 16-bit output tile staged through LDS for whole-line stores
     static constexpr bool kStageOut = BN * BM * 2 <= kLds;
+    // one block fills a CU (4 SIMDs x OCC waves): the LDS beyond the ring is
+    // then free for the epilogue's side area
+    static constexpr bool kOneBlockPerCU = kWaves == 4 * OCC;
+};
+
+constexpr int kLdsPerCU = 160 * 1024;
+
+// Side area of the staged epilogue, after the ring: the block's row scales,
+// channel scales and bias as fp32, [BM xs | BN ws | BN bias].  Each thread
+// loads at most kIters of these values at kernel start (their latency hides
+// under the prologue's tile loads), keeps them in registers through the main
+// loop and writes them here at the epilogue, whose dequantization then reads
+// its scales from LDS instead of issuing global loads after the last MFMA.
+template <class C, int ODT, int MODE>
+struct SideArea {
+    static constexpr int kValues = C::BM + C::BN;
+    static constexpr int kBytesIfUsed = (kValues + C::BN) * 4;
+    static constexpr bool kUse = MODE != 1 && ODT != W8A8_F32 && C::kStageOut && C::kOneBlockPerCU &&
+                                 C::kLds + kBytesIfUsed <= kLdsPerCU;
+    static constexpr int kBytes = kUse ? kBytesIfUsed : 0;
+    static constexpr int kIters = kUse ? (kValues + C::kThreads - 1) / C::kThreads : 1;
 };
 
 // The 16-byte output chunk c of staged row r sits at chunk c ^ (r mod chunks-per-row, up to 32).
@@ -414,44 +435,79 @@ __device__ __forceinline__ int out_swz(int row) {
 // MODE 2 adds the residual in the write-out pass, where the residual row and
 // the scales are read as 16-byte chunks (resid and a per-channel rscale
 // 16-byte aligned, which the caller checks).
-template <int ODT, int MODE, bool GELU, class C>
+template <int ODT, int MODE, bool GELU, class C, class Side>
 __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::TM], int8_t* lds,
                                                    int lane, int t, int m_base, int n_base,
                                                    int wave_m, int wave_n, int M, int N,
                                                    const float* __restrict__ xs,
                                                    const float* __restrict__ ws, int64_t ws_size,
                                                    const void* __restrict__ bias, const Residual& res,
-                                                   void* __restrict__ out) {
+                                                   void* __restrict__ out,
+                                                   const float (&side_v)[Side::kIters],
+                                                   const float (&side_b)[Side::kIters]) {
     constexpr int BN = C::BN, BM = C::BM, TN = C::TN, TM = C::TM;
     constexpr int kRowBytes = BN * 2;
     constexpr int kChunks = BN / 8;   // 16-byte chunks per staged row
     using OS = typename DType<ODT>::storage;
     const int lane_m = lane % 32, half = lane / 32;
+    float* const sv = reinterpret_cast<float*>(lds + C::kLds);   // [BM xs | BN ws]
+    float* const sb = sv + BM + BN;                               // [BN bias]
     float xsv[TM];
-    static_for<0, TM>([&](auto j) {
-        const int m = m_base + wave_m + j * 32 + lane_m;
-        xsv[j] = xs[m < M ? m : M - 1];
-    });
-    __syncthreads();  // every wave has finished reading the last K tile
+    if constexpr (Side::kUse) {
+        static_for<0, Side::kIters>([&](auto it) {
+            const int idx = t + it * C::kThreads;
+            if (idx < BM + BN) {
+                sv[idx] = side_v[it];
+                if (idx >= BM) sb[idx - BM] = side_b[it];
+            }
+        });
+    } else {
+        static_for<0, TM>([&](auto j) {
+            const int m = m_base + wave_m + j * 32 + lane_m;
+            xsv[j] = xs[m < M ? m : M - 1];
+        });
+    }
+    __syncthreads();  // every wave has finished reading the last K tile (and the side area is written)
+    if constexpr (Side::kUse) {
+        static_for<0, TM>([&](auto j) { xsv[j] = sv[wave_m + j * 32 + lane_m]; });
+    }
     static_for<0, TN>([&](auto i) {
         static_for<0, 4>([&](auto g) {
             const int chunk = (wave_n + i * 32 + 8 * g) / 8;
-            const int n0 = n_base + wave_n + i * 32 + 8 * g + 4 * half;
+            const int nl = wave_n + i * 32 + 8 * g + 4 * half;
+            const int n0 = n_base + nl;
             float wsv[4], bv[4];
-            static_for<0, 4>([&](auto e) {
-                const int n = n0 + e < N ? n0 + e : N - 1;
-                wsv[e] = ws[ws_size == 1 ? 0 : n];
-                bv[e] = bias ? DType<ODT>::load(static_cast<const OS*>(bias)[n]) : 0.0f;
-            });
+            if constexpr (Side::kUse) {
+                const float4 w4 = *reinterpret_cast<const float4*>(sv + BM + nl);
+                const float4 b4 = *reinterpret_cast<const float4*>(sb + nl);
+                wsv[0] = w4.x; wsv[1] = w4.y; wsv[2] = w4.z; wsv[3] = w4.w;
+                bv[0] = b4.x; bv[1] = b4.y; bv[2] = b4.z; bv[3] = b4.w;
+            } else {
+                static_for<0, 4>([&](auto e) {
+                    const int n = n0 + e < N ? n0 + e : N - 1;
+                    wsv[e] = ws[ws_size == 1 ? 0 : n];
+                    bv[e] = bias ? DType<ODT>::load(static_cast<const OS*>(bias)[n]) : 0.0f;
+                });
+            }
             static_for<0, TM>([&](auto j) {
                 const int ml = wave_m + j * 32 + lane_m;
-                float v[4];
-                static_for<0, 4>([&](auto e) {
-                    v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
-                });
                 uint2 p;
-                p.x = DType<ODT>::store2(v[0], v[1]);
-                p.y = DType<ODT>::store2(v[2], v[3]);
+                if constexpr (GELU && ODT == W8A8_BF16) {
+                    // round the pre-activations in pairs, then GELU in pairs
+                    float v[4];
+                    static_for<0, 4>([&](auto e) {
+                        v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], false);
+                    });
+                    p.x = gelu_bf16x2(pack2_bf16(v[0], v[1]));
+                    p.y = gelu_bf16x2(pack2_bf16(v[2], v[3]));
+                } else {
+                    float v[4];
+                    static_for<0, 4>([&](auto e) {
+                        v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
+                    });
+                    p.x = DType<ODT>::store2(v[0], v[1]);
+                    p.y = DType<ODT>::store2(v[2], v[3]);
+                }
                 *reinterpret_cast<uint2*>(lds + ml * kRowBytes + (chunk ^ out_swz<BN>(ml)) * 16 + half * 8) = p;
             });
         });
@@ -500,7 +556,8 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     constexpr int TN = C::TN, TM = C::TM, CPR = C::CPR, KS = C::KS;
     constexpr int kTileBytes = C::kTileBytes, kLoadsPerThread = C::kLoadsPerThread;
     constexpr int kWWaveLoads = C::kWWaveLoads;
-    __shared__ __attribute__((aligned(1024))) int8_t lds[C::kLds];
+    using Side = SideArea<C, ODT, MODE>;
+    __shared__ __attribute__((aligned(1024))) int8_t lds[C::kLds + Side::kBytes];
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n, group_m);
@@ -508,6 +565,28 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     // The wave index is uniform across the wave: in an SGPR, so operand choice,
     // buffer resources and LDS destinations of the tile loads stay scalar.
     const int t = threadIdx.x, lane = t % kWave, wave = __builtin_amdgcn_readfirstlane(t / kWave);
+
+    // Epilogue scales of this block (side area): value idx < BM is xs of row
+    // m_base + idx, else ws and bias of channel n_base + idx - BM (clamped to
+    // the last row / channel, as the direct epilogue clamps them).
+    float side_v[Side::kIters], side_b[Side::kIters];
+    if constexpr (Side::kUse) {
+        using OS = typename DType<ODT>::storage;
+        static_for<0, Side::kIters>([&](auto it) {
+            const int idx = t + it * C::kThreads;
+            side_v[it] = 0.0f;
+            side_b[it] = 0.0f;
+            if (idx < BM) {
+                const int m = m_base + idx;
+                side_v[it] = xs[m < M ? m : M - 1];
+            } else if (idx < BM + BN) {
+                int n = n_base + idx - BM;
+                n = n < N ? n : N - 1;
+                side_v[it] = ws[ws_size == 1 ? 0 : n];
+                if (bias) side_b[it] = DType<ODT>::load(static_cast<const OS*>(bias)[n]);
+            }
+        });
+    }
     const int wave_n = (wave % (BN / WN)) * WN;
     const int wave_m = (wave / (BN / WN)) * WM;
     const int KT = K / BK;                                 // K % BK == 0 (host checks)
@@ -671,8 +750,8 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
             vec_ok = vec_ok && (reinterpret_cast<uintptr_t>(res.resid) % 16) == 0 &&
                      (res.rs_size == 1 || (reinterpret_cast<uintptr_t>(res.rscale) % 16) == 0);
         if (vec_ok) {
-            store_tiles_staged<ODT, MODE, GELU, C>(acc, lds, lane, t, m_base, n_base, wave_m, wave_n, M, N,
-                                                   xs, ws, ws_size, bias, res, out);
+            store_tiles_staged<ODT, MODE, GELU, C, Side>(acc, lds, lane, t, m_base, n_base, wave_m, wave_n, M,
+                                                         N, xs, ws, ws_size, bias, res, out, side_v, side_b);
             return;
         }
     }

@@ -310,6 +310,28 @@ def _gelu_close(got, want, odt):
 
 
 @pytest.mark.parametrize("odt", ["bf16", "f16"])
+def test_gemm_gelu_epilogue_every_preactivation(odt):
+    """Every finite 16-bit pre-activation through the GEMM's GELU epilogue.
+    Zero codes make the accumulators 0, so the pre-activation of channel n is
+    fma(0 * xs, ws, bias[n]) = bias[n] exactly; the bias takes every finite bit
+    pattern of the output dtype (the saturated tails, the cancelling negative
+    tail, subnormals and signed zeros included)."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    bits = bits[np.isfinite(O.to_f32(bits, odt))]
+    n = (len(bits) + 255) // 256 * 256
+    bias = np.resize(bits, n)
+    m, k = 64, 128
+    q = torch.zeros(m, k, dtype=torch.int8)
+    w = torch.zeros(n, k, dtype=torch.int8)
+    xs = torch.full((m,), 0.75)
+    ws = torch.full((n,), 1.25)
+    out = W.gemm_dequant(q.to(DEV), w.to(DEV), xs.to(DEV), ws.to(DEV), from_storage(bias, odt),
+                         TD[odt], gelu=True)
+    want = O.epilogue_kitchen(np.zeros((m, n), np.int32), xs.numpy(), ws.numpy(), bias, odt, act=1)
+    _gelu_close(storage(out, odt), want, odt)
+
+
+@pytest.mark.parametrize("odt", ["bf16", "f16"])
 def test_gemv_gelu_epilogue_within_one_ulp(odt):
     m, n, k = 2, 4096, 3072
     x = make_x(m, k, "bf16", seed=21)
