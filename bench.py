@@ -235,7 +235,7 @@ def main():
                    "ffn": FFN, "linears": "qkv 3072->9216, out 3072->3072, up 3072->12288 +gelu_tanh, "
                                          "down 12288->3072; per-token quant of each input included",
                    "parallelism": "single_gpu", "pct_int8_peak": round(100 * value / PEAK_INT8_TOPS, 2)},
-        "roofline": {"kernel": "gemm_mfma_dma DmaCfg<256,192,64,96,128,2,2> (FFN-up 11712x3072x12288, "
+        "roofline": {"kernel": "gemm_mfma_dma DmaCfg<256,256,128,64,128,2,2> (FFN-up 11712x3072x12288, "
                                "bf16 out, GELU epilogue)",
                      "bound": "mfma", "achieved": round(up_tops, 2), "peak": PEAK_INT8_TOPS,
                      "unit": "TOPS", "frac": round(up_tops / PEAK_INT8_TOPS, 4), "traffic": traffic_bytes(),
@@ -255,7 +255,7 @@ def traffic_bytes():
         return None
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         "hbm_traffic_ffn_up_gemm_and_quant_M11712.txt")
-    key = "gemm_mfma_dma DmaCfg<256,192,64,96,128,2,2> ffn_up traffic_bytes_per_launch:"
+    key = "gemm_mfma_dma DmaCfg<256,256,128,64,128,2,2> ffn_up traffic_bytes_per_launch:"
     try:
         with open(path) as f:
             for line in f:

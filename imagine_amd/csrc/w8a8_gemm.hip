@@ -50,7 +50,8 @@ using CfgN256M128 = DmaCfg<256, 128, 128, 64, 64, 3, 2>;
 using CfgN256M256 = DmaCfg<256, 256, 128, 128, 128, 2, 1>;
 
 // W8A8_GEMM_MAINLOOP = n256m192w8 | n256m256w8 | n256m128 | n256m256 | regs
-// selects one (a tuning knob; every choice produces identical results).
+// forces one (a tuning knob; every choice produces identical results).  By
+// default the shape picks between N256M256W8 and N256M192W8 (prefer_n256m256).
 static int mainloop_choice() {
     static int choice = [] {
         const char* e = std::getenv("W8A8_GEMM_MAINLOOP");
@@ -59,6 +60,7 @@ static int mainloop_choice() {
         if (std::strcmp(e, "n256m128") == 0) return 1;
         if (std::strcmp(e, "n256m256") == 0) return 3;
         if (std::strcmp(e, "n256m256w8") == 0) return 4;
+        if (std::strcmp(e, "n256m192w8") == 0) return 6;
         return 5;
     }();
     return choice;
@@ -91,6 +93,35 @@ static void launch_dma(const int8_t* q, const int8_t* w, const float* xs, const 
                            static_cast<int>(K), kGroupM);
 }
 
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Default tile choice between the two one-block-per-CU configurations: the
+// estimated time of a shape is (rounds of tiles over the CUs) x (tile area),
+// divided by the configuration's measured per-area speed.  256 x 256 tiles load
+// 15% fewer bytes per MFMA operation than 256 x 192 and ran ~6% faster per
+// tile area on the FFN-up shape; 256 x 192 cuts M = 11712 exactly and fills
+// the rounds better when there are few tiles (N = 3072: 3 rounds of 732
+// tiles at 95% vs 552 tiles at 72%).
+static bool prefer_n256m256(int64_t M, int64_t N) {
+    const int64_t cus = device_cus();
+    auto cost = [&](int64_t bn, int64_t bm, double speed) {
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        return static_cast<double>((tiles + cus - 1) / cus) * static_cast<double>(bn * bm) / speed;
+    };
+    return cost(256, 256, 1.06) < cost(256, 192, 1.0);
+}
+
 template <int ODT, int MODE, bool GELU>
 static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                     int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
@@ -98,7 +129,11 @@ static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const flo
     const int choice = mainloop_choice();
     // whole K tiles only (the DMA ring has no tail masking)
     if (choice == 0) return false;
-    if (choice == 5 && K % CfgN256M192W8::BK == 0) {
+    if (choice == 5 && K % CfgN256M256W8::BK == 0 && prefer_n256m256(M, N)) {
+        launch_dma<ODT, MODE, GELU, CfgN256M256W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
+        return true;
+    }
+    if ((choice == 5 || choice == 6) && K % CfgN256M192W8::BK == 0) {
         launch_dma<ODT, MODE, GELU, CfgN256M192W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
         return true;
     }
