@@ -18,7 +18,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libw8a8_hip.so"
-SOURCES = ["w8a8_quant.hip", "w8a8_convrot.hip", "w8a8_gemv.hip", "w8a8_gemm.hip", "w8a8_api.hip"]
+SOURCES = ["w8a8_quant.hip", "w8a8_convrot.hip", "w8a8_gemv.hip", "w8a8_gemm.hip", "w8a8_glue.hip",
+           "w8a8_api.hip"]
 ARCH = os.environ.get("W8A8_OFFLOAD_ARCH", "gfx950")
 
 

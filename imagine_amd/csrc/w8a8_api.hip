@@ -35,6 +35,13 @@ void launch_convrot_rotate(const void* x, int x_dtype, void* y, int64_t M, int64
 bool convrot_weight_fused(const void* w, const void* q, int64_t K, int64_t group);
 void launch_quantize_tensorwise(const void* x, int x_dtype, int8_t* q, float* scale, int64_t n, bool given,
                                 bool recip, hipStream_t stream);
+void launch_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
+                  int64_t sg, int64_t tg, float eps, int dtype, bool rms, hipStream_t stream);
+void launch_gated_residual(const void* x, const void* y, const void* gate0, const void* gate1, void* out,
+                           int64_t batch, int64_t tokens, int64_t d, int64_t prefix, int dtype,
+                           hipStream_t stream);
+void launch_quant_modulated(const void* x, int dtype, const void* mod, int8_t* q, float* xs, int64_t M,
+                            int64_t K, int recip, hipStream_t stream);
 }  // namespace w8a8
 
 namespace {
@@ -110,6 +117,45 @@ int w8a8_quantize_rowwise(const void* x, int x_dtype, int8_t* q, float* xs, int6
     w8a8::launch_quantize(x, x_dtype, q, xs, M, K, flags & W8A8_SCALE_RECIP,
                           flags & W8A8_ACT_GELU_TANH, false, stream);
     return check_launch("quantize_int8_rowwise");
+}
+
+int w8a8_quantize_rowwise_modulated(const void* x, int x_dtype, const void* modulation_scale, int8_t* q,
+                                    float* xs, int64_t M, int64_t K, uint32_t flags, hipStream_t stream) {
+    if (int rc = check_common(M, 0, K, flags)) return rc;
+    if (flags & ~W8A8_SCALE_RECIP) return fail(W8A8_ERR_VALUE, "only W8A8_SCALE_RECIP applies to the modulated quantizer");
+    if (!valid_dtype(x_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for INT8 quantization");
+    if (M == 0) return W8A8_OK;
+    if (K > 0 && (!x || !q || !modulation_scale)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (!xs) return fail(W8A8_ERR_VALUE, "null scale pointer");
+    w8a8::launch_quant_modulated(x, x_dtype, modulation_scale, q, xs, M, K, (flags & W8A8_SCALE_RECIP) ? 1 : 0,
+                                 stream);
+    return check_launch("quantize_int8_rowwise_modulated");
+}
+
+int w8a8_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
+               int64_t scale_group, int64_t shift_group, double eps, int dtype, int rms, hipStream_t stream) {
+    if (n < 0 || d < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (d == 0) return fail(W8A8_ERR_VALUE, "integer division or modulo by zero");
+    if (!valid_dtype(dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported dtype for adaln");
+    if (scale_group <= 0 || shift_group <= 0) return fail(W8A8_ERR_VALUE, "modulation group must be positive");
+    if (n == 0) return W8A8_OK;
+    if (!x || !scale || !shift || !out) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (n > 0x7fffffff) return fail(W8A8_ERR_VALUE, "adaln supports at most 2^31 - 1 rows");
+    w8a8::launch_adaln(x, scale, shift, out, n, d, scale_group, shift_group, static_cast<float>(eps), dtype,
+                       rms != 0, stream);
+    return check_launch(rms ? "rms_adaln" : "adaln");
+}
+
+int w8a8_gated_residual(const void* x, const void* y, const void* gate0, const void* gate1, void* out,
+                        int64_t batch, int64_t tokens, int64_t d, int64_t prefix, int dtype, hipStream_t stream) {
+    if (batch < 0 || tokens < 0 || d < 0 || prefix < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (!valid_dtype(dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported dtype for gated_residual");
+    if (batch == 0 || tokens == 0 || d == 0) return W8A8_OK;
+    if (!x || !y || !gate1 || !out || (prefix > 0 && !gate0)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (batch * tokens > 0x7fffffff) return fail(W8A8_ERR_VALUE, "gated_residual supports at most 2^31 - 1 rows");
+    w8a8::launch_gated_residual(x, y, prefix > 0 ? gate0 : gate1, gate1, out, batch, tokens, d, prefix, dtype,
+                                stream);
+    return check_launch("gated_residual");
 }
 
 int w8a8_row_scales(const void* x, int x_dtype, float* xs, int64_t M, int64_t K, uint32_t flags,
@@ -339,7 +385,7 @@ namespace {
 int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
                      const void* bias, const w8a8::Residual* res, void* out, int out_dtype, int64_t M,
                      int64_t N, int64_t K, int64_t convrot_group, uint32_t flags, void* workspace,
-                     int64_t workspace_bytes, hipStream_t stream) {
+                     int64_t workspace_bytes, hipStream_t stream, const void* modulation = nullptr) {
     if (int rc = check_common(M, N, K, flags)) return rc;
     if (flags & W8A8_OUT_INT32) return fail(W8A8_ERR_VALUE, "W8A8_OUT_INT32 is a GEMM-only flag");
     if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
@@ -377,8 +423,11 @@ int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* w
     // Fused route: row scales, then a GEMM that quantizes its activation tiles
     // (an input activation is only applied by the standalone quantizer); a
     // residual is then applied by the standalone residual kernel.
-    if (!convrot_group && !gemv && (flags & W8A8_FUSED_QUANT) && !(qflags & W8A8_ACT_GELU_TANH) && N > 0 &&
-        x_dtype != W8A8_F32 && K % 16 == 0) {
+    if (modulation) {
+        if (int rc = w8a8_quantize_rowwise_modulated(x, x_dtype, modulation, q, xs, M, K, qflags, stream))
+            return rc;
+    } else if (!convrot_group && !gemv && (flags & W8A8_FUSED_QUANT) && !(qflags & W8A8_ACT_GELU_TANH) &&
+               N > 0 && x_dtype != W8A8_F32 && K % 16 == 0) {
         if (int rc = w8a8_row_scales(x, x_dtype, xs, M, K, qflags, stream)) return rc;
         if (w8a8::launch_gemm_xq(x, x_dtype, xs, w, ws, ws_size, bias, out, out_dtype, M, N, K,
                                  false, stream)) {
@@ -387,7 +436,9 @@ int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* w
             return w8a8_residual_apply(out, res->resid, res->rscale, res->rs_size, out_dtype, M, N, stream);
         }
     }
-    if (convrot_group) {
+    if (modulation) {
+        // quantized above
+    } else if (convrot_group) {
         void* rotated = static_cast<char*>(workspace) + (M * K + 255) / 256 * 256 + (M * 4 + 255) / 256 * 256;
         if (int rc = w8a8_quantize_rowwise_convrot(x, x_dtype, q, xs, M, K, convrot_group, qflags, rotated,
                                                    w8a8_convrot_workspace_bytes(M, K, convrot_group, x_dtype),
@@ -427,6 +478,17 @@ int w8a8_int8_linear_residual(const void* x, int x_dtype, const int8_t* w, const
     const w8a8::Residual res{rscale, rscale_size, resid};
     return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, &res, out, out_dtype, M, N, K, 0, flags,
                             workspace, workspace_bytes, stream);
+}
+
+int w8a8_int8_linear_modulated(const void* x, int x_dtype, const void* modulation_scale, const int8_t* w,
+                               const float* ws, int64_t ws_size, const void* bias, void* out, int out_dtype,
+                               int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
+                               int64_t workspace_bytes, hipStream_t stream) {
+    if (flags & (W8A8_ACT_GELU_TANH | W8A8_FUSED_QUANT))
+        return fail(W8A8_ERR_VALUE, "int8_linear_modulated takes no input activation or fused quantization");
+    if (M > 0 && K > 0 && !modulation_scale) return fail(W8A8_ERR_VALUE, "null modulation_scale");
+    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, nullptr, out, out_dtype, M, N, K, 0, flags,
+                            workspace, workspace_bytes, stream, modulation_scale ? modulation_scale : x);
 }
 
 int w8a8_int8_linear_convrot(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,

@@ -1,0 +1,194 @@
+// Block glue of the Qwen-Image DiT around its W8A8 linears, for gfx950.
+//
+//   adaln / rms_adaln   Kitchen's native "adaln" call as the crate issues it
+//                       (inference/src/backend_eager.rs:176-229): per row i of
+//                       x [n, d], out = T(T(T(norm(x_i)) * T(1 + scale_g)) + shift_h)
+//                       with g = i / sg, h = i / tg, the op order of the
+//                       crate's eager route (:186-199: layer_norm or rms_norm,
+//                       mul by scale + 1, add shift, each rounded to T).
+//   gated residual      x += y * gate, tokens before the prefix with gate0,
+//                       the rest with gate1 (models/qwen_image21/numeric.rs:
+//                       110-125, ATen addcmul_: T(fp32(x + y * g))).
+//   modulated quantizer the batch-one modulation of int8_linear_modulated
+//                       (backend_bindings.rs:329-405): xm = T(x * T(1 + s_k)),
+//                       then the per-token quantizer on xm, in one kernel.
+//
+// All three are bandwidth kernels over bf16/fp16/fp32 rows: one 256-thread
+// block per row, 16-byte loads where the row is aligned, fp32 arithmetic.
+#include "w8a8_common.h"
+
+namespace w8a8 {
+
+namespace {
+
+constexpr int kGlueThreads = 256;
+
+__device__ __forceinline__ float block_sum(float v, float* part) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();   // earlier readers of part are done
+    if ((threadIdx.x % kWave) == 0) part[wave] = v;
+    __syncthreads();
+    return (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+// Row element k of a T row, as float.
+template <int DT>
+__device__ __forceinline__ float ld(const void* p, int64_t k) {
+    return DType<DT>::load(static_cast<const typename DType<DT>::storage*>(p)[k]);
+}
+
+template <int DT, bool RMS>
+__global__ __launch_bounds__(kGlueThreads) void adaln_rows(const void* __restrict__ x,
+                                                           const void* __restrict__ scale,
+                                                           const void* __restrict__ shift,
+                                                           void* __restrict__ out, int64_t d,
+                                                           int64_t sg, int64_t tg, float eps) {
+    using D = DType<DT>;
+    using OS = typename D::storage;
+    __shared__ float part[4];
+    const int64_t row = blockIdx.x;
+    const OS* xr = static_cast<const OS*>(x) + row * d;
+    const OS* sr = static_cast<const OS*>(scale) + (row / sg) * d;
+    const OS* hr = static_cast<const OS*>(shift) + (row / tg) * d;
+    OS* o = static_cast<OS*>(out) + row * d;
+    const float inv_d = 1.0f / static_cast<float>(d);
+    float mean = 0.0f, rstd;
+    if constexpr (RMS) {
+        // aten rms_norm: x * rsqrt(mean(x^2) + eps) in fp32
+        float s2 = 0.0f;
+        for (int64_t k = threadIdx.x; k < d; k += kGlueThreads) {
+            const float v = D::load(xr[k]);
+            s2 = fmaf(v, v, s2);
+        }
+        s2 = block_sum(s2, part);
+        rstd = 1.0f / sqrtf(s2 * inv_d + eps);
+    } else {
+        // aten layer_norm: biased variance, rstd = 1 / sqrt(var + eps)
+        float s1 = 0.0f;
+        for (int64_t k = threadIdx.x; k < d; k += kGlueThreads) s1 += D::load(xr[k]);
+        mean = block_sum(s1, part) * inv_d;
+        float s2 = 0.0f;
+        for (int64_t k = threadIdx.x; k < d; k += kGlueThreads) {
+            const float c = D::load(xr[k]) - mean;
+            s2 = fmaf(c, c, s2);
+        }
+        const float var = block_sum(s2, part) * inv_d;
+        rstd = 1.0f / sqrtf(fmaxf(var, 0.0f) + eps);
+    }
+    const float bias = -rstd * mean;   // aten's y = x * rstd + (-rstd * mean)
+    for (int64_t k = threadIdx.x; k < d; k += kGlueThreads) {
+        const float v = D::load(xr[k]);
+        const float y = D::round(RMS ? v * rstd : fmaf(v, rstd, bias));
+        const float m = D::round(1.0f + D::load(sr[k]));
+        const float z = D::round(y * m);
+        o[k] = D::store(z + D::load(hr[k]));
+    }
+}
+
+// x[b, t, :] += y[b, t, :] * gate[b, :], gate = gate0 for t < prefix else gate1;
+// gates are [batch, d].  out may alias x (the reference updates x in place).
+template <int DT>
+__global__ __launch_bounds__(kGlueThreads) void gated_residual_rows(const void* __restrict__ x,
+                                                                    const void* __restrict__ y,
+                                                                    const void* __restrict__ gate0,
+                                                                    const void* __restrict__ gate1,
+                                                                    void* out, int64_t tokens,
+                                                                    int64_t d, int64_t prefix) {
+    using D = DType<DT>;
+    using OS = typename D::storage;
+    const int64_t row = blockIdx.x;   // b * tokens + t
+    const int64_t b = row / tokens, t = row % tokens;
+    const OS* g = static_cast<const OS*>(t < prefix ? gate0 : gate1) + b * d;
+    const OS* xr = static_cast<const OS*>(x) + row * d;
+    const OS* yr = static_cast<const OS*>(y) + row * d;
+    OS* o = static_cast<OS*>(out) + row * d;
+    for (int64_t k = threadIdx.x; k < d; k += kGlueThreads) {
+        // y * g of two 16-bit values is exact in fp32: one fp32 rounding of
+        // the sum, then the rounding to T, as ATen's addcmul.
+        const float v = D::load(xr[k]) + D::load(yr[k]) * D::load(g[k]);
+        o[k] = D::store(v);
+    }
+}
+
+// Modulated per-token quantizer: xm = T(x * T(1 + s_k)), s = modulation_scale[K];
+// scale = max(amax(xm) / 127, 1e-30) (or the CUDA form), codes as the plain
+// quantizer.  xm is recomputed in the code pass (same operations, same bits).
+template <int DT>
+__global__ __launch_bounds__(kGlueThreads) void quant_rows_modulated(const void* __restrict__ x,
+                                                                     const void* __restrict__ mod,
+                                                                     int8_t* __restrict__ q,
+                                                                     float* __restrict__ xs,
+                                                                     int64_t K, int recip) {
+    using D = DType<DT>;
+    using OS = typename D::storage;
+    __shared__ float part[4];
+    const int64_t row = blockIdx.x;
+    const OS* xr = static_cast<const OS*>(x) + row * K;
+    const OS* mr = static_cast<const OS*>(mod);
+    auto xm = [&](int64_t k) { return D::round(D::load(xr[k]) * D::round(1.0f + D::load(mr[k]))); };
+    float amax = 0.0f;
+    for (int64_t k = threadIdx.x; k < K; k += kGlueThreads) amax = fmaxf(amax, fabsf(xm(k)));
+    amax = wave_max(amax);
+    if ((threadIdx.x % kWave) == 0) part[threadIdx.x / kWave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    const float s = row_scale<DT>(amax, recip != 0);
+    if (threadIdx.x == 0) xs[row] = s;
+    const RowQuant rq = row_quant<DT>(s);
+    for (int64_t k = threadIdx.x; k < K; k += kGlueThreads)
+        q[row * K + k] = static_cast<int8_t>(quant_elem<DT>(xm(k), rq));
+}
+
+}  // namespace
+
+void launch_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
+                  int64_t sg, int64_t tg, float eps, int dtype, bool rms, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(n)), block(kGlueThreads);
+#define W8A8_ADALN_CASE(DT)                                                                            \
+    if (dtype == DT) {                                                                                 \
+        if (rms) hipLaunchKernelGGL((adaln_rows<DT, true>), grid, block, 0, stream, x, scale, shift, out, d, sg, tg, eps); \
+        else hipLaunchKernelGGL((adaln_rows<DT, false>), grid, block, 0, stream, x, scale, shift, out, d, sg, tg, eps);    \
+        return;                                                                                        \
+    }
+    W8A8_ADALN_CASE(W8A8_BF16)
+    W8A8_ADALN_CASE(W8A8_F16)
+    W8A8_ADALN_CASE(W8A8_F32)
+#undef W8A8_ADALN_CASE
+}
+
+void launch_gated_residual(const void* x, const void* y, const void* gate0, const void* gate1, void* out,
+                           int64_t batch, int64_t tokens, int64_t d, int64_t prefix, int dtype,
+                           hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(batch * tokens)), block(kGlueThreads);
+    switch (dtype) {
+        case W8A8_BF16:
+            hipLaunchKernelGGL((gated_residual_rows<W8A8_BF16>), grid, block, 0, stream, x, y, gate0, gate1, out, tokens, d, prefix);
+            break;
+        case W8A8_F16:
+            hipLaunchKernelGGL((gated_residual_rows<W8A8_F16>), grid, block, 0, stream, x, y, gate0, gate1, out, tokens, d, prefix);
+            break;
+        default:
+            hipLaunchKernelGGL((gated_residual_rows<W8A8_F32>), grid, block, 0, stream, x, y, gate0, gate1, out, tokens, d, prefix);
+            break;
+    }
+}
+
+void launch_quant_modulated(const void* x, int dtype, const void* mod, int8_t* q, float* xs, int64_t M,
+                            int64_t K, int recip, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(M)), block(kGlueThreads);
+    switch (dtype) {
+        case W8A8_BF16:
+            hipLaunchKernelGGL((quant_rows_modulated<W8A8_BF16>), grid, block, 0, stream, x, mod, q, xs, K, recip);
+            break;
+        case W8A8_F16:
+            hipLaunchKernelGGL((quant_rows_modulated<W8A8_F16>), grid, block, 0, stream, x, mod, q, xs, K, recip);
+            break;
+        default:
+            hipLaunchKernelGGL((quant_rows_modulated<W8A8_F32>), grid, block, 0, stream, x, mod, q, xs, K, recip);
+            break;
+    }
+}
+
+}  // namespace w8a8

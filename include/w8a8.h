@@ -229,6 +229,48 @@ int w8a8_quantize_convrot_weight(const void* w, int w_dtype, int8_t* q, float* s
                                  int64_t K, int64_t group, uint32_t flags, void* rotated,
                                  int64_t rotated_bytes, hipStream_t stream);
 
+/* ---- DiT block glue around the linears ------------------------------------ */
+
+/* Adaptive LayerNorm / RMSNorm with modulation, Kitchen's native "adaln" and
+ * "rms_adaln" calls as the crate issues them (inference/src/backend_eager.rs:
+ * 176-229: input [n, d], scale [n / scale_group, d], shift [n / shift_group, d],
+ * out, n, d, sg, tg, eps, dtype): row i gets scale row i / scale_group and
+ * shift row i / shift_group, and
+ *   out = T( T( T(norm(x)) * T(1 + scale) ) + shift ),
+ * norm = layer_norm without affine (biased variance) or, with rms != 0,
+ * x * rsqrt(mean(x^2) + eps), in fp32: the op order of the crate's eager
+ * route (:186-199).  d == 0 fails with the reference's ZeroDivisionError
+ * text as W8A8_ERR_VALUE. */
+int w8a8_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
+               int64_t scale_group, int64_t shift_group, double eps, int dtype, int rms,
+               hipStream_t stream);
+
+/* Gated residual of the DiT block (inference/src/models/qwen_image21/
+ * numeric.rs:110-125): x, y [batch, tokens, d], gates [batch, d];
+ *   out[b, t] = T( fp32( x[b, t] + y[b, t] * gate[b] ) ),
+ * gate = gate0 for t < prefix, else gate1 (ATen addcmul_ on each slice; y *
+ * gate is exact in fp32 for 16-bit T).  out may equal x (in place, as the
+ * reference). */
+int w8a8_gated_residual(const void* x, const void* y, const void* gate0, const void* gate1, void* out,
+                        int64_t batch, int64_t tokens, int64_t d, int64_t prefix, int dtype,
+                        hipStream_t stream);
+
+/* Per-token quantization of the modulated input of Kitchen's batch-one
+ * int8_linear_modulated (inference/src/backend_bindings.rs:329-405):
+ *   xm = T( x * T(1 + modulation_scale[k]) ),  then w8a8_quantize_rowwise on xm
+ * (modulation_scale: K values in x's dtype), in one kernel.  Flags:
+ * W8A8_SCALE_RECIP. */
+int w8a8_quantize_rowwise_modulated(const void* x, int x_dtype, const void* modulation_scale, int8_t* q,
+                                    float* xs, int64_t M, int64_t K, uint32_t flags, hipStream_t stream);
+
+/* int8_linear_modulated (backend_bindings.rs:329-405): int8_linear of the
+ * modulated input above, same routes, workspace (w8a8_int8_linear_workspace_bytes)
+ * and epilogue as w8a8_int8_linear.  Flags: W8A8_SCALE_RECIP, W8A8_ROUTE_GEMM. */
+int w8a8_int8_linear_modulated(const void* x, int x_dtype, const void* modulation_scale, const int8_t* w,
+                               const float* ws, int64_t ws_size, const void* bias, void* out, int out_dtype,
+                               int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
+                               int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

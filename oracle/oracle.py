@@ -235,3 +235,39 @@ def linear_kitchen(x, x_dtype, w, ws, bias, out_dtype, scale_mode=0, input_act=0
     acc = gemm_i32(q, w)
     out = epilogue_kitchen(acc, xs, ws, bias, out_dtype, contract=contract, act=epilogue_act)
     return out, q, xs, acc
+
+
+# ---------------------------------------------------------------- DiT block glue
+# Bit-level restatements (numpy) of the glue's elementwise steps.  Each product
+# of two 16-bit values is exact in fp32, so these are single roundings.
+
+def modulate(x, s, dtype):
+    """backend_bindings.rs:391-394 on storage arrays: T(x * T(1 + s)), s of
+    x's last-dim width broadcast over the rows."""
+    xf = to_f32(x, dtype)
+    m = to_f32(to_dtype(np.float32(1.0) + to_f32(s, dtype), dtype), dtype)
+    return to_dtype((xf * m).astype(np.float32), dtype)
+
+
+def gated_residual(x, y, g, dtype):
+    """numeric.rs:110-125 (ATen addcmul_) on storage arrays: T(fp32(x + y * g))."""
+    v = (to_f32(x, dtype) + to_f32(y, dtype) * to_f32(g, dtype)).astype(np.float32)
+    return to_dtype(v, dtype)
+
+
+def adaln(x, scale, shift, eps, dtype, rms=False):
+    """backend_eager.rs:186-199 in float64 up to the roundings of the op order:
+    y = T(norm(x)), T(y * T(1 + scale)), T(. + shift); x [n, d], scale and shift
+    broadcast against it.  The fp32 reductions of the reference round the mean
+    and rstd differently, so this matches it to within one ulp of T."""
+    xf = to_f32(x, dtype).astype(np.float64)
+    if rms:
+        y = xf / np.sqrt((xf * xf).mean(axis=-1, keepdims=True) + eps)
+    else:
+        mu = xf.mean(axis=-1, keepdims=True)
+        var = ((xf - mu) ** 2).mean(axis=-1, keepdims=True)
+        y = (xf - mu) / np.sqrt(var + eps)
+    y = to_f32(to_dtype(y.astype(np.float32), dtype), dtype)
+    m = to_f32(to_dtype(np.float32(1.0) + to_f32(scale, dtype), dtype), dtype)
+    z = to_f32(to_dtype((y * m).astype(np.float32), dtype), dtype)
+    return to_dtype((z + to_f32(shift, dtype)).astype(np.float32), dtype)

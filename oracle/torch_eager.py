@@ -67,3 +67,43 @@ def int8_linear(x, weight, weight_scale, bias=None, out_dtype=torch.bfloat16, in
     if bias is not None:
         out = out + bias.to(out_dtype).reshape(1, -1)
     return out.reshape(*shape[:-1], weight.shape[0]), q, xs, acc
+
+
+# ---------------------------------------------------------------- DiT block glue
+# The reference's eager (CPU) routes of the glue around the linears, as the same
+# ATen ops in the same order.
+
+def adaln(x, scale, shift, eps, rms=False):
+    """backend_eager.rs:186-199: norm over the last dim (layer_norm without
+    affine, or rms_norm without weight), * (scale + 1), + shift; every op in
+    x's dtype."""
+    shape = [x.shape[-1]]
+    if rms:
+        normalized = torch.nn.functional.rms_norm(x, shape, None, eps)
+    else:
+        normalized = torch.nn.functional.layer_norm(x, shape, None, None, eps)
+    return normalized.mul(scale.add(1)).add(shift)
+
+
+def modulated_norm(x, scale, prefix, zero, eps):
+    """numeric.rs:63-107 (inference branch) with the eager adaln."""
+    out = adaln(x, scale[1], zero, eps)
+    if prefix != 0:
+        out[:, :prefix].copy_(adaln(x[:, :prefix], scale[0], zero, eps))
+    return out
+
+
+def gated_residual(x, y, gate, prefix):
+    """numeric.rs:110-125: in-place addcmul_ on the two token ranges."""
+    x[:, prefix:].addcmul_(y[:, prefix:], gate[1])
+    if prefix != 0:
+        x[:, :prefix].addcmul_(y[:, :prefix], gate[0])
+    return x
+
+
+def modulate(x, modulation_scale):
+    """backend_bindings.rs:391-394: x * (modulation_scale + 1), the scale
+    reshaped to broadcast over x's leading dims."""
+    width = x.shape[-1]
+    shape = [1] * (x.dim() - 1) + [width]
+    return x.mul(modulation_scale.reshape(shape).add(1.0))

@@ -1,0 +1,136 @@
+"""GPU parity of the DiT block glue kernels (w8a8_glue.hip) against the
+reference's eager ATen op sequences (oracle/torch_eager.py) and the oracle.
+
+Bar: the modulated quantizer's codes and scales and the modulated linear's
+outputs bit-exact; the gated residual bit-exact for 16-bit dtypes (fp32 within
+one ulp); adaLN within one ulp of the norm carried through its two roundings,
+and at least 97% of outputs bit-equal (the fp32 mean / variance reductions
+round in a different order than ATen's)."""
+import numpy as np
+import pytest
+import torch
+
+import imagine_amd as W
+from oracle import oracle as O
+from oracle import torch_eager as E
+
+pytestmark = pytest.mark.gpu
+TD = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    W._lib.load()
+    yield
+    torch.cuda.synchronize()
+
+
+def storage(t, dtype):
+    t = t.detach().cpu().contiguous()
+    return t.numpy() if dtype == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+
+
+def close(got, want, dtype, frac=0.97, before_add=None):
+    """Two ulps of the larger of the result and the value before the last
+    addition (``before_add``: adaLN's T(norm * (1 + scale)), where a shift
+    of the opposite sign cancels), and ``frac`` of the outputs bit-equal."""
+    a = O.to_f32(got, dtype).astype(np.float64)
+    b = O.to_f32(want, dtype).astype(np.float64)
+    mag = np.abs(b) if before_add is None else np.maximum(np.abs(b), np.abs(before_add))
+    rel = {"bf16": 2.0**-7, "f16": 2.0**-10, "f32": 2.0**-22}[dtype]
+    bad = np.abs(a - b) > 2 * mag * rel + 1e-6
+    assert not bad.any(), f"{int(bad.sum())} outputs off; e.g. got {a[bad][:4]} want {b[bad][:4]}"
+    assert (got == want).mean() > frac
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("rms", [False, True])
+def test_adaln_matches_eager_sequence(dtype, rms):
+    g = torch.Generator().manual_seed(41)
+    x = (torch.randn(2, 300, 3072, generator=g) * 2 + 0.25).to(TD[dtype])
+    scale = (torch.randn(2, 1, 3072, generator=g) * 0.5).to(TD[dtype])
+    shift = (torch.randn(2, 1, 3072, generator=g) * 0.1).to(TD[dtype])
+    print(f"adaln {dtype} rms={rms} x={tuple(x.shape)}", flush=True)
+    out = W.adaln(x.to(DEV), scale.to(DEV), shift.to(DEV), 1e-6, rms=rms)
+    want = E.adaln(x, scale, shift, 1e-6, rms)
+    z = E.adaln(x, scale, torch.zeros_like(shift), 1e-6, rms).float().numpy()
+    # fp32 outputs carry the reduction-order differences unrounded: ulp bound only
+    close(storage(out, dtype), storage(want, dtype), dtype, frac=0.0 if dtype == "f32" else 0.97,
+          before_add=z)
+
+
+def test_adaln_per_token_modulation_and_odd_width():
+    """scale with one row per token (group 1), a width that is no multiple of
+    the block size, and a [1, d] shift shared by all rows."""
+    g = torch.Generator().manual_seed(42)
+    x = (torch.randn(3, 7, 1000, generator=g)).to(torch.bfloat16)
+    scale = (torch.randn(3, 7, 1000, generator=g) * 0.3).to(torch.bfloat16)
+    shift = (torch.randn(1000, generator=g) * 0.3).to(torch.bfloat16)
+    out = W.adaln(x.to(DEV), scale.to(DEV), shift.to(DEV), 1e-5)
+    want = E.adaln(x, scale, shift, 1e-5)
+    z = E.adaln(x, scale, torch.zeros_like(shift), 1e-5).float().numpy()
+    close(storage(out, "bf16"), storage(want, "bf16"), "bf16", before_add=z)
+
+
+def test_modulated_norm_with_text_prefix():
+    """The DiT's norm1/norm2: text tokens (the prefix) take the first
+    modulation, image tokens the second; shift zero."""
+    g = torch.Generator().manual_seed(43)
+    x = (torch.randn(2, 512, 3072, generator=g)).to(torch.bfloat16)
+    s0 = (torch.randn(2, 1, 3072, generator=g) * 0.4).to(torch.bfloat16)
+    s1 = (torch.randn(2, 1, 3072, generator=g) * 0.4).to(torch.bfloat16)
+    zero = torch.zeros(2, 1, 3072, dtype=torch.bfloat16)
+    out = W.modulated_norm(x.to(DEV), (s0.to(DEV), s1.to(DEV)), 256, zero.to(DEV), 1e-6)
+    want = E.modulated_norm(x, (s0, s1), 256, zero, 1e-6)
+    close(storage(out, "bf16"), storage(want, "bf16"), "bf16")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("prefix", [0, 256])
+def test_gated_residual_matches_addcmul(dtype, prefix):
+    g = torch.Generator().manual_seed(44 + prefix)
+    x = (torch.randn(2, 700, 3072, generator=g) * 3).to(TD[dtype])
+    y = (torch.randn(2, 700, 3072, generator=g) * 2).to(TD[dtype])
+    g0 = torch.randn(2, 1, 3072, generator=g).to(TD[dtype])
+    g1 = torch.randn(2, 1, 3072, generator=g).to(TD[dtype])
+    xd = x.to(DEV)
+    ret = W.gated_residual(xd, y.to(DEV), (g0.to(DEV), g1.to(DEV)), prefix)
+    assert ret.data_ptr() == xd.data_ptr()   # in place, as the reference
+    want = E.gated_residual(x.clone(), y, (g0, g1), prefix)
+    if dtype == "f32":
+        close(storage(xd, dtype), storage(want, dtype), dtype, frac=0.0)
+    else:
+        assert np.array_equal(storage(xd, dtype), storage(want, dtype))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_modulated_quantizer_bit_exact(dtype):
+    g = torch.Generator().manual_seed(45)
+    x = (torch.randn(333, 3072, generator=g) * 2).to(TD[dtype])
+    x[3] = 0
+    s = (torch.randn(3072, generator=g) * 0.6).to(TD[dtype])
+    q, xs = W.quantize_rowwise_modulated(x.to(DEV), s.to(DEV))
+    xm = O.modulate(storage(x, dtype), storage(s, dtype), dtype)
+    q_ref, xs_ref = O.quant_rowwise(xm, dtype)
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(xs.cpu().numpy().reshape(-1), xs_ref)
+
+
+@pytest.mark.parametrize("m", [1, 2, 300])
+def test_int8_linear_modulated_bit_exact(m):
+    """GEMV (M = 1, 2) and GEMM routes: the linear of the modulated input with
+    the reference CUDA routes' epilogue, bit for bit; default out dtype bf16."""
+    g = torch.Generator().manual_seed(46 + m)
+    k, n = 3072, 1024
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    s = (torch.randn(k, generator=g) * 0.5).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    ws = torch.rand(n, generator=g) * 9e-3 + 1e-3
+    b = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16)
+    out = W.int8_linear_modulated(x.to(DEV), s.to(DEV), w.to(DEV), ws.to(DEV), b.to(DEV))
+    assert out.dtype == torch.bfloat16
+    xm = O.modulate(storage(x, "bf16"), storage(s, "bf16"), "bf16")
+    want, _, _, _ = O.linear_kitchen(xm, "bf16", w.numpy(), ws.numpy(), storage(b, "bf16"), "bf16")
+    assert np.array_equal(storage(out, "bf16"), want)
