@@ -322,6 +322,34 @@ def measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv):
                                         "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
                                         "bytes": per, "buffer_sets": nsets}
     del ws_
+    # block glue at the DiT block's hidden states [2, 5856, 3072] bf16 (the
+    # norm1/norm2 adaLN and the two gated residuals), rotating sets
+    hb, ht = 2, M_TOK // 2
+    hbytes = hb * ht * HID * 2
+    per = 2 * hbytes                       # adaLN: read x, write out
+    nsets = max(2, int(1.2e9 // per) + 1)
+    hx = [torch.randn(hb, ht, HID, device=dev).to(torch.bfloat16) for _ in range(nsets)]
+    ho = [torch.empty_like(hx[0]) for _ in range(nsets)]
+    hs = (torch.randn(hb, 1, HID, device=dev) * 0.3).to(torch.bfloat16)
+    hz = torch.zeros(hb, 1, HID, device=dev, dtype=torch.bfloat16)
+    def adaln(i):
+        j = i % nsets
+        W._lib.check(lib.w8a8_adaln(hx[j].data_ptr(), hs.data_ptr(), hz.data_ptr(), ho[j].data_ptr(), hb * ht,
+                                    HID, ht, ht, 1e-6, W._lib.BF16, 0, stream()))
+    ms = median_of_batches(adaln)
+    ex["adaln_2x5856x3072"] = {"us": round(ms * 1e3, 2), "GB/s": round(per / (ms * 1e-3) / 1e9, 1),
+                               "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+                               "bytes": per, "buffer_sets": nsets}
+    per = 3 * hbytes                       # gated residual: read x and y, write x
+    def gres(i):
+        j = i % nsets
+        W._lib.check(lib.w8a8_gated_residual(hx[j].data_ptr(), ho[j].data_ptr(), hs.data_ptr(), hs.data_ptr(),
+                                             hx[j].data_ptr(), hb, ht, HID, 256, W._lib.BF16, stream()))
+    ms = median_of_batches(gres)
+    ex["gated_residual_2x5856x3072"] = {"us": round(ms * 1e3, 2), "GB/s": round(per / (ms * 1e-3) / 1e9, 1),
+                                        "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+                                        "bytes": per, "buffer_sets": nsets}
+    del hx, ho
     # outlier workload: fused quant+GEMM vs unfused
     m, k, n = M_TOK, HID, FFN
     x = student_t(m, k, 3).to(dev)

@@ -13,8 +13,13 @@
 //                       (backend_bindings.rs:329-405): xm = T(x * T(1 + s_k)),
 //                       then the per-token quantizer on xm, in one kernel.
 //
-// All three are bandwidth kernels over bf16/fp16/fp32 rows: one 256-thread
-// block per row, 16-byte loads where the row is aligned, fp32 arithmetic.
+// All three are bandwidth kernels over bf16/fp16/fp32 rows, fp32 arithmetic.
+// adaln: one 256-thread block per row; aligned rows of up to 2048 16-byte
+// chunks stay in registers (CPL chunks per lane) between the reduction passes
+// and the output pass, so x is read once; other rows take a generic kernel
+// that re-reads the row.  Gated residual: 16-byte chunks, grid-stride.
+#include <algorithm>
+
 #include "w8a8_common.h"
 
 namespace w8a8 {
@@ -31,12 +36,6 @@ __device__ __forceinline__ float block_sum(float v, float* part) {
     if ((threadIdx.x % kWave) == 0) part[wave] = v;
     __syncthreads();
     return (part[0] + part[1]) + (part[2] + part[3]);
-}
-
-// Row element k of a T row, as float.
-template <int DT>
-__device__ __forceinline__ float ld(const void* p, int64_t k) {
-    return DType<DT>::load(static_cast<const typename DType<DT>::storage*>(p)[k]);
 }
 
 template <int DT, bool RMS>
@@ -87,6 +86,88 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows(const void* __restric
     }
 }
 
+// Register-resident adaln: lane chunk c = tid + j * 256 of the row (E values
+// per 16-byte chunk); same operations per element as adaln_rows, so the same
+// results up to the order of the fp32 row sums.
+template <int DT, bool RMS, int CPL>
+__global__ __launch_bounds__(kGlueThreads) void adaln_rows_vec(const void* __restrict__ x,
+                                                               const void* __restrict__ scale,
+                                                               const void* __restrict__ shift,
+                                                               void* __restrict__ out, int64_t d,
+                                                               int64_t sg, int64_t tg, float eps) {
+    using D = DType<DT>;
+    constexpr int E = 16 / D::bytes;
+    __shared__ float part[4];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t nchunks = d / E;
+    const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * d * D::bytes);
+    const uint4* sr = reinterpret_cast<const uint4*>(static_cast<const char*>(scale) + (row / sg) * d * D::bytes);
+    const uint4* hr = reinterpret_cast<const uint4*>(static_cast<const char*>(shift) + (row / tg) * d * D::bytes);
+    uint4* o = reinterpret_cast<uint4*>(static_cast<char*>(out) + row * d * D::bytes);
+    uint4 raw[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        raw[j] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
+    }
+    auto elem = [&](const uint4& v, int i) {
+        return D::load(reinterpret_cast<const typename D::storage*>(&v)[i]);
+    };
+    const float inv_d = 1.0f / static_cast<float>(d);
+    float mean = 0.0f, rstd;
+    if constexpr (RMS) {
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const float v = elem(raw[j], i);
+                s2 = fmaf(v, v, s2);
+            }
+        s2 = block_sum(s2, part);
+        rstd = 1.0f / sqrtf(s2 * inv_d + eps);
+    } else {
+        float s1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int i = 0; i < E; ++i) s1 += elem(raw[j], i);
+        mean = block_sum(s1, part) * inv_d;
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+            if (c >= nchunks) break;   // padding chunks are zeros, not row values
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const float cv = elem(raw[j], i) - mean;
+                s2 = fmaf(cv, cv, s2);
+            }
+        }
+        const float var = block_sum(s2, part) * inv_d;
+        rstd = 1.0f / sqrtf(fmaxf(var, 0.0f) + eps);
+    }
+    const float bias = -rstd * mean;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        if (c >= nchunks) break;
+        const uint4 sv = sr[c], hv = hr[c];
+        uint4 res;
+        typename D::storage* rp = reinterpret_cast<typename D::storage*>(&res);
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const float v = elem(raw[j], i);
+            const float y = D::round(RMS ? v * rstd : fmaf(v, rstd, bias));
+            const float m = D::round(1.0f + elem(sv, i));
+            const float z = D::round(y * m);
+            rp[i] = D::store(z + elem(hv, i));
+        }
+        o[c] = res;
+    }
+}
+
 // x[b, t, :] += y[b, t, :] * gate[b, :], gate = gate0 for t < prefix else gate1;
 // gates are [batch, d].  out may alias x (the reference updates x in place).
 template <int DT>
@@ -109,6 +190,33 @@ __global__ __launch_bounds__(kGlueThreads) void gated_residual_rows(const void* 
         // the sum, then the rounding to T, as ATen's addcmul.
         const float v = D::load(xr[k]) + D::load(yr[k]) * D::load(g[k]);
         o[k] = D::store(v);
+    }
+}
+
+// The same over 16-byte chunks (d % E == 0, 16-byte aligned operands): chunk
+// c of the [rows, d] tensor lies in row c / (d / E).
+template <int DT>
+__global__ __launch_bounds__(kGlueThreads) void gated_residual_vec(const uint4* __restrict__ x,
+                                                                   const uint4* __restrict__ y,
+                                                                   const uint4* __restrict__ gate0,
+                                                                   const uint4* __restrict__ gate1,
+                                                                   uint4* out, int64_t tokens, int64_t dc,
+                                                                   int64_t prefix, int64_t total) {
+    using D = DType<DT>;
+    constexpr int E = 16 / D::bytes;
+    for (int64_t c = static_cast<int64_t>(blockIdx.x) * kGlueThreads + threadIdx.x; c < total;
+         c += static_cast<int64_t>(gridDim.x) * kGlueThreads) {
+        const int64_t row = c / dc, k = c % dc;
+        const int64_t b = row / tokens, t = row % tokens;
+        const uint4 xv = x[c], yv = y[c], gv = (t < prefix ? gate0 : gate1)[b * dc + k];
+        const typename D::storage* xe = reinterpret_cast<const typename D::storage*>(&xv);
+        const typename D::storage* ye = reinterpret_cast<const typename D::storage*>(&yv);
+        const typename D::storage* ge = reinterpret_cast<const typename D::storage*>(&gv);
+        uint4 res;
+        typename D::storage* re = reinterpret_cast<typename D::storage*>(&res);
+#pragma unroll
+        for (int i = 0; i < E; ++i) re[i] = D::store(D::load(xe[i]) + D::load(ye[i]) * D::load(ge[i]));
+        out[c] = res;
     }
 }
 
@@ -143,11 +251,45 @@ __global__ __launch_bounds__(kGlueThreads) void quant_rows_modulated(const void*
 
 }  // namespace
 
+namespace {
+
+template <int DT, bool RMS, int CPL>
+void launch_adaln_vec(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
+                      int64_t sg, int64_t tg, float eps, hipStream_t stream) {
+    hipLaunchKernelGGL((adaln_rows_vec<DT, RMS, CPL>), dim3(static_cast<unsigned>(n)), dim3(kGlueThreads), 0,
+                       stream, x, scale, shift, out, d, sg, tg, eps);
+}
+
+template <int DT, bool RMS>
+bool adaln_vec_dispatch(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
+                        int64_t sg, int64_t tg, float eps, hipStream_t stream) {
+    constexpr int E = 16 / DType<DT>::bytes;
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (d % E != 0 || !al(x) || !al(scale) || !al(shift) || !al(out)) return false;
+    const int64_t per_lane = (d / E + kGlueThreads - 1) / kGlueThreads;
+    switch (per_lane) {
+        case 1: launch_adaln_vec<DT, RMS, 1>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        case 2: launch_adaln_vec<DT, RMS, 2>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        case 3: launch_adaln_vec<DT, RMS, 3>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        case 4: launch_adaln_vec<DT, RMS, 4>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        case 5:
+        case 6: launch_adaln_vec<DT, RMS, 6>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        case 7:
+        case 8: launch_adaln_vec<DT, RMS, 8>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        default: return false;
+    }
+}
+
+}  // namespace
+
 void launch_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
                   int64_t sg, int64_t tg, float eps, int dtype, bool rms, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(n)), block(kGlueThreads);
 #define W8A8_ADALN_CASE(DT)                                                                            \
     if (dtype == DT) {                                                                                 \
+        if (rms ? adaln_vec_dispatch<DT, true>(x, scale, shift, out, n, d, sg, tg, eps, stream)        \
+                : adaln_vec_dispatch<DT, false>(x, scale, shift, out, n, d, sg, tg, eps, stream))      \
+            return;                                                                                    \
         if (rms) hipLaunchKernelGGL((adaln_rows<DT, true>), grid, block, 0, stream, x, scale, shift, out, d, sg, tg, eps); \
         else hipLaunchKernelGGL((adaln_rows<DT, false>), grid, block, 0, stream, x, scale, shift, out, d, sg, tg, eps);    \
         return;                                                                                        \
@@ -162,6 +304,27 @@ void launch_gated_residual(const void* x, const void* y, const void* gate0, cons
                            int64_t batch, int64_t tokens, int64_t d, int64_t prefix, int dtype,
                            hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(batch * tokens)), block(kGlueThreads);
+    const int esz = dtype == W8A8_F32 ? 4 : 2, E = 16 / esz;
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (d % E == 0 && al(x) && al(y) && al(gate0) && al(gate1) && al(out)) {
+        const int64_t dc = d / E, total = batch * tokens * dc;
+        const int64_t blocks = std::min<int64_t>((total + kGlueThreads - 1) / kGlueThreads, 256 * 16);
+        const dim3 vgrid(static_cast<unsigned>(blocks));
+        const uint4 *xv = static_cast<const uint4*>(x), *yv = static_cast<const uint4*>(y);
+        const uint4 *g0 = static_cast<const uint4*>(gate0), *g1 = static_cast<const uint4*>(gate1);
+        uint4* ov = static_cast<uint4*>(out);
+        switch (dtype) {
+            case W8A8_BF16:
+                hipLaunchKernelGGL((gated_residual_vec<W8A8_BF16>), vgrid, block, 0, stream, xv, yv, g0, g1, ov, tokens, dc, prefix, total);
+                return;
+            case W8A8_F16:
+                hipLaunchKernelGGL((gated_residual_vec<W8A8_F16>), vgrid, block, 0, stream, xv, yv, g0, g1, ov, tokens, dc, prefix, total);
+                return;
+            default:
+                hipLaunchKernelGGL((gated_residual_vec<W8A8_F32>), vgrid, block, 0, stream, xv, yv, g0, g1, ov, tokens, dc, prefix, total);
+                return;
+        }
+    }
     switch (dtype) {
         case W8A8_BF16:
             hipLaunchKernelGGL((gated_residual_rows<W8A8_BF16>), grid, block, 0, stream, x, y, gate0, gate1, out, tokens, d, prefix);
