@@ -13,11 +13,13 @@ divided by the step time, quantization included in the time).
 Also measured and reported beside it: per-linear TOPS, the per-token
 quantizer's GB/s (M=11712, K=3072 and K=12288), the adaLN GEMV's GB/s
 (M=2, K=3072, N=18432), and fused vs unfused quant+GEMM on the outlier
-workload (M=11712, K=3072, N=12288, Student-t(3) activations).  The memory-
-bound kernels rotate through enough buffer sets to exceed the 256 MB Infinity
-Cache so they measure HBM, not cache.
+workload (M=11712, K=3072, N=12288, Student-t(3) activations), the block
+glue's GB/s (adaLN, gated residual at 2x5856x3072), and the 60-block DiT
+denoising step at M=19904 (ms/step, W8A8 and glue shares; attention, QK
+RMSNorm and RoPE in torch).  The memory-bound kernels rotate through enough
+buffer sets to exceed the 256 MB Infinity Cache so they measure HBM, not cache.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--only KERNEL] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--only KERNEL] [--no-cpu] [--no-dit-step]
 """
 import argparse
 import json
@@ -43,8 +45,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--only", default=None,
                    help="run only one kernel in a loop (for rocprofv3 counters): "
-                        "up_gemm | quant | convrot_quant | step | copy")
+                        "up_gemm | quant | convrot_quant | step | copy | dit_step")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-dit-step", action="store_true", help="skip the 60-block DiT step extra")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     return p.parse_args()
 
@@ -203,6 +206,9 @@ def main():
             up_timer.stop(s)
         quant(outs["up"], qbuf[FFN]); gemm(qbuf[FFN], layers[3], outs["down"], False)
 
+    if args.only == "dit_step":
+        print(json.dumps(measure_dit_step(W, dev, steps=max(args.steps, 1), warmup=args.warmup)), flush=True)
+        return
     if args.only:
         run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs)
         return
@@ -225,6 +231,8 @@ def main():
           f"-> {up_tops:.1f} TOPS", file=sys.stderr, flush=True)
 
     extras = measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv)
+    if not args.no_dit_step:
+        extras["dit_step_60_blocks_M19904"] = measure_dit_step(W, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": "W8A8 GEMM TOPS (% INT8 MFMA peak) at Qwen-DiT 1600x896 shapes; quant GB/s",
@@ -373,6 +381,106 @@ def measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv):
         "unfused_us": round(mu * 1e3, 1), "fused_us": round(mf * 1e3, 1),
         "unfused_TOPS": round(ops / (mu * 1e-3) / 1e12, 1), "fused_TOPS": round(ops / (mf * 1e-3) / 1e12, 1)}
     return ex
+
+
+def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
+    """The 60-block Qwen-Image-style MMDiT denoising step: hidden 3072, 24 heads
+    x 128, FFN 12288 (GELU-tanh), a 1600x896 latent (5600 tokens) + one 1 MP
+    reference image (4096) + 256 text tokens, CFG batch 2 (M = 19904), on
+    random-init int8 weights (60 distinct sets, ~6.8 GB, resident in HBM).
+    Per block, as the reference's block forward (models/qwen_image21/dit.rs:
+    285-340): text and image modulation GEMVs (M=2, N=18432) -> norm1
+    (modulated_norm, text prefix 256) -> QKV -> QK RMSNorm + RoPE (torch bf16)
+    -> attention (torch fused SDPA; no math fallback) -> out-proj -> gated
+    residual -> norm2 -> FFN-up -> FFN-down with input_act gelu_tanh -> gated
+    residual.  Every linear goes through imagine_amd.int8_linear (quantizer +
+    GEMM/GEMV) and the glue through imagine_amd.glue.  HIP events around each
+    library call inside the timed steps give the W8A8 and glue shares."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    B, T_txt = 2, 256
+    T = 5600 + 4096 + T_txt
+    D, H, HD = HID, 24, 128
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(4)
+
+    def lin(k, n):
+        w = torch.randint(-127, 128, (n, k), device=dev, dtype=torch.int8, generator=g)
+        ws = torch.rand(n, device=dev, generator=g) * 9e-3 + 1e-3
+        b = (torch.randn(n, device=dev, generator=g) * 0.02).to(bf)
+        return w, ws, b
+
+    blks = [{"mod_txt": lin(D, 6 * D), "mod_img": lin(D, 6 * D), "qkv": lin(D, 3 * D), "out": lin(D, D),
+             "up": lin(D, FFN), "down": lin(FFN, D),
+             "qn": (1 + 0.1 * torch.randn(HD, device=dev, generator=g)).to(bf),
+             "kn": (1 + 0.1 * torch.randn(HD, device=dev, generator=g)).to(bf)} for _ in range(blocks)]
+    temb = torch.nn.functional.silu(torch.randn(B, D, device=dev, generator=g)).to(bf)
+    x0 = torch.randn(B, T, D, device=dev, generator=g).to(bf)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, HD, 2, device=dev).float() / HD))
+    ang = torch.arange(T, device=dev).float()[:, None] * inv[None]
+    cos = ang.cos().to(bf)[None, :, None, :]
+    sin = ang.sin().to(bf)[None, :, None, :]
+    zero = torch.zeros(B, 1, D, device=dev, dtype=bf)
+    ev = {"w8a8": [], "glue": []}
+
+    def timed(kind, fn, *a, **k):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        r = fn(*a, **k)
+        e.record()
+        ev[kind].append((s, e))
+        return r
+
+    def rope(t):
+        t1, t2 = t[..., 0::2], t[..., 1::2]
+        return torch.stack((t1 * cos - t2 * sin, t1 * sin + t2 * cos), dim=-1).flatten(-2)
+
+    def block(x, p):
+        mt = [c.reshape(B, 1, D).contiguous() for c in timed("w8a8", W.int8_linear, temb, *p["mod_txt"]).chunk(6, -1)]
+        mi = [c.reshape(B, 1, D).contiguous() for c in timed("w8a8", W.int8_linear, temb, *p["mod_img"]).chunk(6, -1)]
+        n1 = timed("glue", W.modulated_norm, x, (mt[1], mi[1]), T_txt, zero, 1e-6)
+        qkv = timed("w8a8", W.int8_linear, n1.reshape(B * T, D), *p["qkv"]).view(B, T, 3, H, HD)
+        q = rope(torch.nn.functional.rms_norm(qkv[:, :, 0], (HD,), p["qn"], 1e-6))
+        k = rope(torch.nn.functional.rms_norm(qkv[:, :, 1], (HD,), p["kn"], 1e-6))
+        v = qkv[:, :, 2]
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            o = torch.nn.functional.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2),
+                                                                 v.transpose(1, 2))
+        o = o.transpose(1, 2).reshape(B * T, D)
+        a = timed("w8a8", W.int8_linear, o, *p["out"])
+        x = timed("glue", W.gated_residual, x, a.view(B, T, D), (mt[2], mi[2]), T_txt)
+        n2 = timed("glue", W.modulated_norm, x, (mt[4], mi[4]), T_txt, zero, 1e-6)
+        up = timed("w8a8", W.int8_linear, n2.reshape(B * T, D), *p["up"])
+        d = timed("w8a8", W.int8_linear, up, *p["down"], input_act="gelu_tanh")
+        return timed("glue", W.gated_residual, x, d.view(B, T, D), (mt[5], mi[5]), T_txt)
+
+    def step():
+        x = x0.clone()
+        for p in blks:
+            x = block(x, p)
+        return x
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev["w8a8"].clear()
+    ev["glue"].clear()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        out = step()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / steps
+    w8 = sum(a.elapsed_time(b) for a, b in ev["w8a8"]) / steps
+    gl = sum(a.elapsed_time(b) for a, b in ev["glue"]) / steps
+    ops = blocks * 2 * (B * T * D * (3 * D + D + FFN) + B * T * FFN * D + 2 * B * D * 6 * D)
+    finite = bool(torch.isfinite(out).all())
+    del blks
+    return {"ms_per_step": round(ms, 2), "w8a8_ms": round(w8, 2), "w8a8_share": round(w8 / ms, 3),
+            "w8a8_TOPS": round(ops / (w8 * 1e-3) / 1e12, 1), "glue_ms": round(gl, 2),
+            "glue_share": round(gl / ms, 3), "blocks": blocks, "M": B * T, "steps": steps,
+            "output_finite": finite,
+            "rest": "QK RMSNorm, RoPE and attention (fused SDPA) in torch bf16"}
 
 
 def run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs):
