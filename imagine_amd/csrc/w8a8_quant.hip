@@ -50,10 +50,29 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
     }
     auto elem = [&](int r, int j, int i) {
         const typename D::storage* e = reinterpret_cast<const typename D::storage*>(&raw[r][j]);
-        float f = D::load(e[i]);
-        if constexpr (GELU) f = D::round(gelu_tanh(f));
-        return f;
+        return D::load(e[i]);
     };
+    // The input activation once per element: raw holds T(gelu_tanh(x)) from
+    // here on (exactly representable in T), so both passes read activated
+    // values without evaluating the activation again.
+    if constexpr (GELU) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                uint32_t* wv = reinterpret_cast<uint32_t*>(&raw[r][j]);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    if constexpr (D::bytes == 4) {
+                        wv[h] = __float_as_uint(gelu_tanh(__uint_as_float(wv[h])));
+                    } else {
+                        const float lo = D::load(static_cast<typename D::storage>(wv[h] & 0xffffu));
+                        const float hi = D::load(static_cast<typename D::storage>(wv[h] >> 16));
+                        wv[h] = D::store2(gelu_tanh(lo), gelu_tanh(hi));
+                    }
+                }
+            }
+    }
 
     float amax[RPW];
 #pragma unroll
