@@ -134,3 +134,29 @@ def test_int8_linear_modulated_bit_exact(m):
     xm = O.modulate(storage(x, "bf16"), storage(s, "bf16"), "bf16")
     want, _, _, _ = O.linear_kitchen(xm, "bf16", w.numpy(), ws.numpy(), storage(b, "bf16"), "bf16")
     assert np.array_equal(storage(out, "bf16"), want)
+
+
+def test_glue_full_size_sampled_rows():
+    """The DiT step's shape, [2, 9952, 3072] bf16 with the 256-token text
+    prefix: modulated_norm and the gated residual on the GPU, 64 sampled token
+    rows of each batch checked against the reference's ATen sequence on the
+    CPU (rows are independent), and the whole output finite."""
+    g = torch.Generator().manual_seed(47)
+    B, T, D, P = 2, 9952, 3072, 256
+    x = torch.randn(B, T, D, generator=g).to(torch.bfloat16)
+    y = (torch.randn(B, T, D, generator=g) * 0.5).to(torch.bfloat16)
+    s0, s1, g0, g1 = ((torch.randn(B, 1, D, generator=g) * 0.3).to(torch.bfloat16) for _ in range(4))
+    zero = torch.zeros(B, 1, D, dtype=torch.bfloat16)
+    rows = torch.cat([torch.arange(0, 4), torch.arange(P - 2, P + 2),
+                      torch.randperm(T, generator=g)[:56]]).sort().values
+    norm = W.modulated_norm(x.to(DEV), (s0.to(DEV), s1.to(DEV)), P, zero.to(DEV), 1e-6)
+    assert bool(torch.isfinite(norm).all())
+    xs = x[:, rows]
+    pref = int((rows < P).sum())
+    want = E.modulated_norm(xs.clone(), (s0, s1), pref, zero, 1e-6)
+    z = E.modulated_norm(xs.clone(), (s0, s1), pref, zero, 1e-6).float().numpy()
+    close(storage(norm[:, rows.to(DEV)], "bf16"), storage(want, "bf16"), "bf16", before_add=z)
+    xd = x.to(DEV)
+    W.gated_residual(xd, y.to(DEV), (g0.to(DEV), g1.to(DEV)), P)
+    want = E.gated_residual(xs.clone(), y[:, rows], (g0, g1), pref)
+    assert np.array_equal(storage(xd[:, rows.to(DEV)], "bf16"), storage(want, "bf16"))
