@@ -114,6 +114,25 @@ def test_quantize_gelu_input_act(dtype):
     assert sd.max() <= 2.0**-7
 
 
+def test_quantize_gelu_vector_and_generic_kernels_agree_for_every_bf16():
+    """The bf16 GELU input activation of the vector quantizer (activated once,
+    in registers, paired rounding) against the generic kernel's per-element
+    evaluation, for all 65536 bf16 bit patterns: row i repeats pattern i eight
+    times, so its scale |T(gelu(x))| / 127 and its codes expose the activated
+    value.  An unaligned copy routes the same rows to the generic kernel."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    rows = np.repeat(bits[:, None], 8, axis=1)
+    xa = from_storage(rows, "bf16")
+    buf = torch.empty(rows.size + 8, dtype=torch.bfloat16, device=DEV)
+    xu = buf[1:1 + rows.size].view(rows.shape)
+    xu.copy_(xa)
+    assert xa.data_ptr() % 16 == 0 and xu.data_ptr() % 16 != 0
+    qa, sa = W.quantize_rowwise(xa, input_act="gelu_tanh")
+    qu, su = W.quantize_rowwise(xu, input_act="gelu_tanh")
+    assert np.array_equal(sa.cpu().numpy().view(np.uint32), su.cpu().numpy().view(np.uint32))
+    assert np.array_equal(qa.cpu().numpy(), qu.cpu().numpy())
+
+
 def test_row_scales_equal_quantizer_scales():
     x = make_x(100, 3072, "bf16", seed=9).to(DEV)
     _, s = W.quantize_rowwise(x)
