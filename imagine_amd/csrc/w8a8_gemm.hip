@@ -44,14 +44,19 @@ bool gemm_mfma_supported(const void* a, size_t a_elem, const int8_t* w, int64_t 
 //               K tiles (72 KB), two blocks per CU.
 //   N256M256:   4 waves of 128 x 128, 2-stage ring of 128-byte tiles, one wave
 //               per SIMD.
+//   N384M192W8: 8 waves of 96 x 96 on a 384 x 192 tile, 2-stage ring of
+//               128-byte K tiles (144 KB of LDS, the staged output exactly
+//               fills it), one block per CU.
 using CfgN256M192W8 = DmaCfg<256, 192, 64, 96, 128, 2, 2>;
 using CfgN256M256W8 = DmaCfg<256, 256, 128, 64, 128, 2, 2>;
+using CfgN384M192W8 = DmaCfg<384, 192, 96, 96, 128, 2, 2>;
 using CfgN256M128 = DmaCfg<256, 128, 128, 64, 64, 3, 2>;
 using CfgN256M256 = DmaCfg<256, 256, 128, 128, 128, 2, 1>;
 
-// W8A8_GEMM_MAINLOOP = n256m192w8 | n256m256w8 | n256m128 | n256m256 | regs
+// W8A8_GEMM_MAINLOOP = n256m192w8 | n256m256w8 | n384m192w8 | n256m128 | n256m256 | regs
 // forces one (a tuning knob; every choice produces identical results).  By
-// default the shape picks between N256M256W8 and N256M192W8 (prefer_n256m256).
+// default the shape picks among N256M192W8, N256M256W8 and N384M192W8
+// (default_tile).
 static int mainloop_choice() {
     static int choice = [] {
         const char* e = std::getenv("W8A8_GEMM_MAINLOOP");
@@ -61,6 +66,7 @@ static int mainloop_choice() {
         if (std::strcmp(e, "n256m256") == 0) return 3;
         if (std::strcmp(e, "n256m256w8") == 0) return 4;
         if (std::strcmp(e, "n256m192w8") == 0) return 6;
+        if (std::strcmp(e, "n384m192w8") == 0) return 7;
         return 5;
     }();
     return choice;
@@ -106,20 +112,24 @@ static int device_cus() {
     return cus[dev];
 }
 
-// Default tile choice between the two one-block-per-CU configurations: the
+// Default tile choice among the three one-block-per-CU configurations: the
 // estimated time of a shape is (rounds of tiles over the CUs) x (tile area),
-// divided by the configuration's measured per-area speed.  256 x 256 tiles load
-// 15% fewer bytes per MFMA operation than 256 x 192 and ran ~6% faster per
-// tile area on the FFN-up shape; 256 x 192 cuts M = 11712 exactly and fills
-// the rounds better when there are few tiles (N = 3072: 3 rounds of 732
-// tiles at 95% vs 552 tiles at 72%).
-static bool prefer_n256m256(int64_t M, int64_t N) {
+// divided by the configuration's measured per-area speed (relative to
+// 256 x 192 at the DiT shapes: 256 x 256 1.06, 384 x 192 1.045; both load
+// 15% fewer bytes per MFMA operation than 256 x 192).  192-token tiles cut
+// M = 11712 exactly; 384 x 192 tiles fill the N = 3072 GEMMs in 2 rounds of
+// 488 tiles (95%), where 256 x 256 makes 552 tiles (3 rounds, 72% full).
+// Returns 0 (256 x 192), 1 (256 x 256) or 2 (384 x 192).
+static int default_tile(int64_t M, int64_t N) {
     const int64_t cus = device_cus();
     auto cost = [&](int64_t bn, int64_t bm, double speed) {
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         return static_cast<double>((tiles + cus - 1) / cus) * static_cast<double>(bn * bm) / speed;
     };
-    return cost(256, 256, 1.06) < cost(256, 192, 1.0);
+    const double c0 = cost(256, 192, 1.0), c1 = cost(256, 256, 1.06), c2 = cost(384, 192, 1.045);
+    if (c1 < c0 && c1 <= c2) return 1;
+    if (c2 < c0) return 2;
+    return 0;
 }
 
 template <int ODT, int MODE, bool GELU>
@@ -129,8 +139,13 @@ static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const flo
     const int choice = mainloop_choice();
     // whole K tiles only (the DMA ring has no tail masking)
     if (choice == 0) return false;
-    if (choice == 5 && K % CfgN256M256W8::BK == 0 && prefer_n256m256(M, N)) {
+    const int tile = choice == 5 ? default_tile(M, N) : -1;
+    if (tile == 1 && K % CfgN256M256W8::BK == 0) {
         launch_dma<ODT, MODE, GELU, CfgN256M256W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
+        return true;
+    }
+    if ((tile == 2 || choice == 7) && K % CfgN384M192W8::BK == 0) {
+        launch_dma<ODT, MODE, GELU, CfgN384M192W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
         return true;
     }
     if ((choice == 5 || choice == 6) && K % CfgN256M192W8::BK == 0) {

@@ -422,11 +422,14 @@ struct SideArea {
     static constexpr int kIters = kUse ? (kValues + C::kThreads - 1) / C::kThreads : 1;
 };
 
-// The 16-byte output chunk c of staged row r sits at chunk c ^ (r mod chunks-per-row, up to 32).
+// The 16-byte output chunk c of staged row r sits at chunk c ^ (r mod P), P
+// the largest power of two up to 32 dividing the chunks per row (48 for
+// 384-wide tiles: P = 16), so the swizzled chunk stays inside its row.
 template <int BN>
 __device__ __forceinline__ int out_swz(int row) {
     constexpr int kChunks = BN / 8;
-    return row & ((kChunks < 32 ? kChunks : 32) - 1);
+    constexpr int kPeriod = kChunks % 32 == 0 ? 32 : kChunks % 16 == 0 ? 16 : kChunks % 8 == 0 ? 8 : 1;
+    return row & (kPeriod - 1);
 }
 
 // Dequantize the block's accumulators into the LDS ring as a BM x BN tile of

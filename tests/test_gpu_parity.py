@@ -248,9 +248,48 @@ def test_gemm_full_size_sampled_rows_bit_exact():
     assert torch.isfinite(out.float()).all()
 
 
+@pytest.mark.parametrize("mode", ["bf16", "bf16_gelu", "f16", "f32", "bf16_residual", "int32"])
+def test_gemm_n3072_tiles_sampled_rows(mode):
+    """M = 11712, N = 3072 (the out-proj / FFN-down width, where the default
+    tile choice takes 384 x 192 tiles), K = 512: every epilogue mode on 64
+    sampled rows against the oracle (GELU within one ulp, the rest bit-exact)."""
+    m, k, n = 11712, 512, 3072
+    odt = {"bf16_gelu": "bf16", "bf16_residual": "bf16", "int32": "f32"}.get(mode, mode)
+    x = make_x(m, k, "bf16", seed=61)
+    w = make_w(n, k, seed=62)
+    g = torch.Generator().manual_seed(63)
+    ws = (torch.rand(n, generator=g) * 9e-3 + 1e-3).float()
+    bias = (torch.randn(n, generator=g) * 0.5).to(TD[odt])
+    xd, wd = x.to(DEV), w.to(DEV)
+    q, xs = W.quantize_rowwise(xd)
+    rows = np.sort(np.random.default_rng(1).choice(m, 64, replace=False))
+    rows[0], rows[-1] = 0, m - 1
+    q_ref, xs_ref = O.quant_rowwise(storage(x[rows], "bf16"), "bf16")
+    acc_ref = O.gemm_i32(q_ref, w.numpy())
+    if mode == "int32":
+        acc = W.gemm_i32(q, wd)
+        assert np.array_equal(acc.cpu().numpy()[rows], acc_ref)
+        return
+    if mode == "bf16_residual":
+        resid, rscale = _residual_inputs(m, n, "bf16", seed=64)
+        out = W.gemm_dequant_residual(q, wd, xs, ws.to(DEV), bias.to(DEV), torch.bfloat16, resid.to(DEV),
+                                      rscale.to(DEV))
+        lin = O.epilogue_kitchen(acc_ref, xs_ref, ws.numpy(), storage(bias, "bf16"), "bf16")
+        want = O.residual(lin, storage(resid, "bf16")[rows], storage(rscale, "bf16"), "bf16")
+        assert np.array_equal(storage(out, "bf16")[rows], want)
+        return
+    out = W.gemm_dequant(q, wd, xs, ws.to(DEV), bias.to(DEV), TD[odt], gelu=mode == "bf16_gelu")
+    want = O.epilogue_kitchen(acc_ref, xs_ref, ws.numpy(), storage(bias, odt), odt,
+                              act=1 if mode == "bf16_gelu" else 0)
+    if mode == "bf16_gelu":
+        _gelu_close(storage(out, odt)[rows], want, odt)
+    else:
+        assert np.array_equal(storage(out, odt)[rows], want)
+
+
 # ---------------------------------------------------------------- GEMV
 
-GEMV_SHAPES = [(2, 18432, 3072), (1, 4, 3072), (2, 17, 16), (1, 129, 6144), (2, 4, 2560),
+GEMV_SHAPES =[(2, 18432, 3072), (1, 4, 3072), (2, 17, 16), (1, 129, 6144), (2, 4, 2560),
                (1, 33, 20), (2, 5, 64), (2, 300, 12288), (1, 64, 2564)]
 
 
