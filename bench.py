@@ -393,9 +393,13 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
     (modulated_norm, text prefix 256) -> QKV -> QK RMSNorm + RoPE (torch bf16)
     -> attention (torch fused SDPA; no math fallback) -> out-proj -> gated
     residual -> norm2 -> FFN-up -> FFN-down with input_act gelu_tanh -> gated
-    residual.  Every linear goes through imagine_amd.int8_linear (quantizer +
-    GEMM/GEMV) and the glue through imagine_amd.glue.  HIP events around each
-    library call inside the timed steps give the W8A8 and glue shares."""
+    residual.  norm1 and norm2 only feed QKV and FFN-up, so they run as the
+    fused norm + quantizer (modulated_norm_quant, the same codes as norm then
+    quantize) followed by the GEMM; the other linears go through
+    imagine_amd.int8_linear (quantizer + GEMM/GEMV), the residuals through
+    imagine_amd.glue.  HIP events around each library call inside the timed
+    steps give the W8A8 (GEMM, GEMV, quantizer), fused norm + quantizer and
+    glue shares."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
     B, T_txt = 2, 256
     T = 5600 + 4096 + T_txt
@@ -420,7 +424,7 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
     cos = ang.cos().to(bf)[None, :, None, :]
     sin = ang.sin().to(bf)[None, :, None, :]
     zero = torch.zeros(B, 1, D, device=dev, dtype=bf)
-    ev = {"w8a8": [], "glue": []}
+    ev = {"w8a8": [], "glue": [], "norm_quant": []}
 
     def timed(kind, fn, *a, **k):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -437,8 +441,9 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
     def block(x, p):
         mt = [c.reshape(B, 1, D).contiguous() for c in timed("w8a8", W.int8_linear, temb, *p["mod_txt"]).chunk(6, -1)]
         mi = [c.reshape(B, 1, D).contiguous() for c in timed("w8a8", W.int8_linear, temb, *p["mod_img"]).chunk(6, -1)]
-        n1 = timed("glue", W.modulated_norm, x, (mt[1], mi[1]), T_txt, zero, 1e-6)
-        qkv = timed("w8a8", W.int8_linear, n1.reshape(B * T, D), *p["qkv"]).view(B, T, 3, H, HD)
+        q1, s1 = timed("norm_quant", W.modulated_norm_quant, x, (mt[1], mi[1]), T_txt, zero, 1e-6)
+        qkv = timed("w8a8", W.gemm_dequant, q1, p["qkv"][0], s1, *p["qkv"][1:], torch.bfloat16)
+        qkv = qkv.view(B, T, 3, H, HD)
         q = rope(torch.nn.functional.rms_norm(qkv[:, :, 0], (HD,), p["qn"], 1e-6))
         k = rope(torch.nn.functional.rms_norm(qkv[:, :, 1], (HD,), p["kn"], 1e-6))
         v = qkv[:, :, 2]
@@ -448,8 +453,8 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
         o = o.transpose(1, 2).reshape(B * T, D)
         a = timed("w8a8", W.int8_linear, o, *p["out"])
         x = timed("glue", W.gated_residual, x, a.view(B, T, D), (mt[2], mi[2]), T_txt)
-        n2 = timed("glue", W.modulated_norm, x, (mt[4], mi[4]), T_txt, zero, 1e-6)
-        up = timed("w8a8", W.int8_linear, n2.reshape(B * T, D), *p["up"])
+        q2, s2 = timed("norm_quant", W.modulated_norm_quant, x, (mt[4], mi[4]), T_txt, zero, 1e-6)
+        up = timed("w8a8", W.gemm_dequant, q2, p["up"][0], s2, *p["up"][1:], torch.bfloat16)
         d = timed("w8a8", W.int8_linear, up, *p["down"], input_act="gelu_tanh")
         return timed("glue", W.gated_residual, x, d.view(B, T, D), (mt[5], mi[5]), T_txt)
 
@@ -462,8 +467,8 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    ev["w8a8"].clear()
-    ev["glue"].clear()
+    for v in ev.values():
+        v.clear()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
     for _ in range(steps):
@@ -473,12 +478,14 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
     ms = s.elapsed_time(e) / steps
     w8 = sum(a.elapsed_time(b) for a, b in ev["w8a8"]) / steps
     gl = sum(a.elapsed_time(b) for a, b in ev["glue"]) / steps
+    nq = sum(a.elapsed_time(b) for a, b in ev["norm_quant"]) / steps
     ops = blocks * 2 * (B * T * D * (3 * D + D + FFN) + B * T * FFN * D + 2 * B * D * 6 * D)
     finite = bool(torch.isfinite(out).all())
     del blks
     return {"ms_per_step": round(ms, 2), "w8a8_ms": round(w8, 2), "w8a8_share": round(w8 / ms, 3),
             "w8a8_TOPS": round(ops / (w8 * 1e-3) / 1e12, 1), "glue_ms": round(gl, 2),
-            "glue_share": round(gl / ms, 3), "blocks": blocks, "M": B * T, "steps": steps,
+            "glue_share": round(gl / ms, 3), "norm_quant_ms": round(nq, 2), "norm_quant_share": round(nq / ms, 3),
+            "blocks": blocks, "M": B * T, "steps": steps,
             "output_finite": finite,
             "rest": "QK RMSNorm, RoPE and attention (fused SDPA) in torch bf16"}
 

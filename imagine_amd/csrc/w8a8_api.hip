@@ -42,6 +42,9 @@ void launch_gated_residual(const void* x, const void* y, const void* gate0, cons
                            hipStream_t stream);
 void launch_quant_modulated(const void* x, int dtype, const void* mod, int8_t* q, float* xs, int64_t M,
                             int64_t K, int recip, hipStream_t stream);
+bool launch_modnorm_quant(const void* x, const void* s0, const void* s1, const void* h0, const void* h1, int8_t* q,
+                          float* xs, int64_t rows, int64_t tokens, int64_t d, int64_t prefix, float eps, int dtype,
+                          bool rms, int recip, hipStream_t stream);
 }  // namespace w8a8
 
 namespace {
@@ -144,6 +147,26 @@ int w8a8_adaln(const void* x, const void* scale, const void* shift, void* out, i
     w8a8::launch_adaln(x, scale, shift, out, n, d, scale_group, shift_group, static_cast<float>(eps), dtype,
                        rms != 0, stream);
     return check_launch(rms ? "rms_adaln" : "adaln");
+}
+
+int w8a8_modulated_norm_quant(const void* x, const void* scale0, const void* scale1, const void* shift0,
+                              const void* shift1, int8_t* q, float* xs, int64_t batch, int64_t tokens, int64_t d,
+                              int64_t prefix, double eps, int dtype, int rms, uint32_t flags, hipStream_t stream) {
+    if (batch < 0 || tokens < 0 || d < 0 || prefix < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (d == 0) return fail(W8A8_ERR_VALUE, "integer division or modulo by zero");
+    if (flags & ~W8A8_SCALE_RECIP) return fail(W8A8_ERR_VALUE, "only W8A8_SCALE_RECIP applies to the fused norm quantizer");
+    if (!valid_dtype(dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported dtype for adaln");
+    if (batch == 0 || tokens == 0) return W8A8_OK;
+    if (!x || !scale1 || !shift1 || !q || !xs || (prefix > 0 && (!scale0 || !shift0)))
+        return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (batch * tokens > 0x7fffffff) return fail(W8A8_ERR_VALUE, "modulated_norm_quant supports at most 2^31 - 1 rows");
+    const void* s0 = prefix > 0 ? scale0 : scale1;
+    const void* h0 = prefix > 0 ? shift0 : shift1;
+    if (!w8a8::launch_modnorm_quant(x, s0, scale1, h0, shift1, q, xs, batch * tokens, tokens, d, prefix,
+                                    static_cast<float>(eps), dtype, rms != 0, (flags & W8A8_SCALE_RECIP) ? 1 : 0,
+                                    stream))
+        return fail(W8A8_ERR_VALUE, "modulated_norm_quant needs 16-byte aligned rows of at most 2048 16-byte chunks");
+    return check_launch("modulated_norm_quant");
 }
 
 int w8a8_gated_residual(const void* x, const void* y, const void* gate0, const void* gate1, void* out,

@@ -168,6 +168,115 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows_vec(const void* __res
     }
 }
 
+// Modulated norm fused with the per-token quantizer, for a norm whose only
+// consumer is an INT8 linear (the DiT's norm1 -> QKV and norm2 -> FFN-up):
+// row r = b * tokens + t of x gets scale / shift rows b of (scale0, shift0)
+// for t < prefix, else of (scale1, shift1) (modulated_norm's text prefix in
+// one launch); its T outputs, computed exactly as adaln_rows_vec computes
+// them, replace the raw row in registers, and their codes and row scale are
+// those the quantizer gives for the stored output.
+template <int DT, bool RMS, int CPL>
+__global__ __launch_bounds__(kGlueThreads) void modnorm_quant_rows_vec(
+    const void* __restrict__ x, const void* __restrict__ scale0, const void* __restrict__ scale1,
+    const void* __restrict__ shift0, const void* __restrict__ shift1, int8_t* __restrict__ q,
+    float* __restrict__ xs, int64_t tokens, int64_t d, int64_t prefix, float eps, int recip) {
+    using D = DType<DT>;
+    using OS = typename D::storage;
+    constexpr int E = 16 / D::bytes;
+    __shared__ float part[4];
+    const int64_t row = blockIdx.x;
+    const int64_t b = row / tokens, t = row % tokens;
+    const int tid = threadIdx.x;
+    const int64_t nchunks = d / E;
+    const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + row * d * D::bytes);
+    const uint4* sr = reinterpret_cast<const uint4*>(static_cast<const char*>(t < prefix ? scale0 : scale1) +
+                                                     b * d * D::bytes);
+    const uint4* hr = reinterpret_cast<const uint4*>(static_cast<const char*>(t < prefix ? shift0 : shift1) +
+                                                     b * d * D::bytes);
+    uint4 raw[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        raw[j] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
+    }
+    auto elem = [&](const uint4& v, int i) { return D::load(reinterpret_cast<const OS*>(&v)[i]); };
+    const float inv_d = 1.0f / static_cast<float>(d);
+    float mean = 0.0f, rstd;
+    if constexpr (RMS) {
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const float v = elem(raw[j], i);
+                s2 = fmaf(v, v, s2);
+            }
+        s2 = block_sum(s2, part);
+        rstd = 1.0f / sqrtf(s2 * inv_d + eps);
+    } else {
+        float s1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int i = 0; i < E; ++i) s1 += elem(raw[j], i);
+        mean = block_sum(s1, part) * inv_d;
+        float s2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+            if (c >= nchunks) break;
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const float cv = elem(raw[j], i) - mean;
+                s2 = fmaf(cv, cv, s2);
+            }
+        }
+        const float var = block_sum(s2, part) * inv_d;
+        rstd = 1.0f / sqrtf(fmaxf(var, 0.0f) + eps);
+    }
+    const float bias = -rstd * mean;
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        if (c >= nchunks) break;
+        const uint4 sv = sr[c], hv = hr[c];
+        OS* rp = reinterpret_cast<OS*>(&raw[j]);
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const float v = elem(raw[j], i);
+            const float y = D::round(RMS ? v * rstd : fmaf(v, rstd, bias));
+            const float m = D::round(1.0f + elem(sv, i));
+            const float z = D::round(y * m);
+            rp[i] = D::store(z + elem(hv, i));
+            amax = fmaxf(amax, fabsf(D::load(rp[i])));
+        }
+    }
+    amax = wave_max(amax);
+    __syncthreads();   // block_sum's readers of part are done
+    if ((tid % kWave) == 0) part[tid / kWave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    const float s = row_scale<DT>(amax, recip != 0);
+    if (tid == 0) xs[row] = s;
+    const RowQuant rq = row_quant<DT>(s);
+    int8_t* qr = q + row * d;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        if (c >= nchunks) break;
+        if constexpr (E == 8) {
+            uint2 packed;
+            packed.x = quant4_packed<DT>(elem(raw[j], 0), elem(raw[j], 1), elem(raw[j], 2), elem(raw[j], 3), rq);
+            packed.y = quant4_packed<DT>(elem(raw[j], 4), elem(raw[j], 5), elem(raw[j], 6), elem(raw[j], 7), rq);
+            *reinterpret_cast<uint2*>(qr + c * E) = packed;
+        } else {
+            *reinterpret_cast<uint32_t*>(qr + c * E) =
+                quant4_packed<DT>(elem(raw[j], 0), elem(raw[j], 1), elem(raw[j], 2), elem(raw[j], 3), rq);
+        }
+    }
+}
+
 // x[b, t, :] += y[b, t, :] * gate[b, :], gate = gate0 for t < prefix else gate1;
 // gates are [batch, d].  out may alias x (the reference updates x in place).
 template <int DT>
@@ -281,6 +390,49 @@ bool adaln_vec_dispatch(const void* x, const void* scale, const void* shift, voi
 }
 
 }  // namespace
+
+namespace {
+
+template <int DT, bool RMS>
+bool modnorm_quant_dispatch(const void* x, const void* s0, const void* s1, const void* h0, const void* h1,
+                            int8_t* q, float* xs, int64_t rows, int64_t tokens, int64_t d, int64_t prefix,
+                            float eps, int recip, hipStream_t stream) {
+    constexpr int E = 16 / DType<DT>::bytes;
+    auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (d % E != 0 || !al(x) || !al(s0) || !al(s1) || !al(h0) || !al(h1) || reinterpret_cast<uintptr_t>(q) % E != 0)
+        return false;
+    const int64_t per_lane = (d / E + kGlueThreads - 1) / kGlueThreads;
+    const dim3 grid(static_cast<unsigned>(rows)), block(kGlueThreads);
+#define W8A8_MNQ(CPL) hipLaunchKernelGGL((modnorm_quant_rows_vec<DT, RMS, CPL>), grid, block, 0, stream, x, s0, s1, h0, h1, q, xs, tokens, d, prefix, eps, recip)
+    switch (per_lane) {
+        case 1: W8A8_MNQ(1); return true;
+        case 2: W8A8_MNQ(2); return true;
+        case 3: W8A8_MNQ(3); return true;
+        case 4: W8A8_MNQ(4); return true;
+        case 5:
+        case 6: W8A8_MNQ(6); return true;
+        case 7:
+        case 8: W8A8_MNQ(8); return true;
+        default: return false;
+    }
+#undef W8A8_MNQ
+}
+
+}  // namespace
+
+bool launch_modnorm_quant(const void* x, const void* s0, const void* s1, const void* h0, const void* h1, int8_t* q,
+                          float* xs, int64_t rows, int64_t tokens, int64_t d, int64_t prefix, float eps, int dtype,
+                          bool rms, int recip, hipStream_t stream) {
+#define W8A8_MNQ_CASE(DT)                                                                                         \
+    if (dtype == DT)                                                                                              \
+        return rms ? modnorm_quant_dispatch<DT, true>(x, s0, s1, h0, h1, q, xs, rows, tokens, d, prefix, eps, recip, stream) \
+                   : modnorm_quant_dispatch<DT, false>(x, s0, s1, h0, h1, q, xs, rows, tokens, d, prefix, eps, recip, stream);
+    W8A8_MNQ_CASE(W8A8_BF16)
+    W8A8_MNQ_CASE(W8A8_F16)
+    W8A8_MNQ_CASE(W8A8_F32)
+#undef W8A8_MNQ_CASE
+    return false;
+}
 
 void launch_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
                   int64_t sg, int64_t tg, float eps, int dtype, bool rms, hipStream_t stream) {

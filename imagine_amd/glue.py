@@ -71,13 +71,13 @@ def adaln(x, scale, shift, eps, rms=False):
     return out.reshape(shape)
 
 
-def modulated_norm(x, scale, prefix, zero, eps):
+def modulated_norm(x, scale, prefix, zero, eps, rms=False):
     """numeric.rs:63-107 (inference branch): adaln of every token with
     ``scale[1]``, then the first ``prefix`` tokens (dimension 1) again with
-    ``scale[0]``; shift ``zero``."""
-    out = adaln(x, scale[1], zero, eps)
+    ``scale[0]``; shift ``zero``.  ``rms`` selects rms_adaln."""
+    out = adaln(x, scale[1], zero, eps, rms=rms)
     if prefix != 0:
-        out[:, :prefix].copy_(adaln(x[:, :prefix], scale[0], zero, eps))
+        out[:, :prefix].copy_(adaln(x[:, :prefix], scale[0], zero, eps, rms=rms))
     return out
 
 
@@ -166,4 +166,36 @@ def quantize_rowwise_modulated(x, modulation_scale, scale_form="ieee"):
     _lib.check(_lib.load().w8a8_quantize_rowwise_modulated(
         _ptr(x2), _dtype_code(x2.dtype, "INT8 quantization"), _ptr(modulation_scale.reshape(-1).contiguous()),
         _ptr(q), _ptr(s), m, k, _lib.SCALE_RECIP if scale_form == "recip" else 0, _stream(x.device)))
+    return q, s
+
+
+def modulated_norm_quant(x, scale, prefix, shift, eps, rms=False, *, scale_form="ieee"):
+    """``modulated_norm`` (numeric.rs:63-107) followed by the per-token INT8
+    quantizer of the linear that consumes it, for x [batch, tokens, d]:
+    returns (q int8 [batch * tokens, d], s fp32 [batch * tokens, 1]), equal bit
+    for bit to ``quantize_rowwise(modulated_norm(x, scale, prefix, shift, eps))``.
+    One kernel when the rows fit its register layout (16-byte aligned, at most
+    2048 16-byte chunks), else those two steps.  ``shift`` is the one shift
+    tensor of both token ranges, as the reference's ``zero``."""
+    from .ops import quantize_rowwise
+    _require_cuda(x, *scale, shift)
+    if x.dim() != 3:
+        raise RuntimeError("modulated_norm_quant: x must be [batch, tokens, d]")
+    if any(t.dtype != x.dtype for t in (*scale, shift)):
+        raise RuntimeError("modulated_norm_quant: scale and shift must have the dtype of x")
+    batch, tokens, d = x.shape
+    esz = x.element_size()
+    x = x.contiguous()
+    s0, s1, h = _gate_rows(scale[0], batch, d), _gate_rows(scale[1], batch, d), _gate_rows(shift, batch, d)
+    fits = (d * esz) % 16 == 0 and d * esz // 16 <= 2048 and x.data_ptr() % 16 == 0
+    if not fits:
+        n = modulated_norm(x, scale, prefix, shift, eps, rms=rms)
+        return quantize_rowwise(n.reshape(batch * tokens, d), scale_form=scale_form)
+    q = torch.empty((batch * tokens, d), dtype=torch.int8, device=x.device)
+    s = torch.empty((batch * tokens, 1), dtype=torch.float32, device=x.device)
+    p = max(0, min(int(prefix), tokens))
+    _lib.check(_lib.load().w8a8_modulated_norm_quant(
+        _ptr(x), _ptr(s0), _ptr(s1), _ptr(h), _ptr(h), _ptr(q), _ptr(s), batch, tokens, d, p, float(eps),
+        _dtype_code(x.dtype, "adaln"), 1 if rms else 0, _lib.SCALE_RECIP if scale_form == "recip" else 0,
+        _stream(x.device)))
     return q, s

@@ -245,6 +245,21 @@ int w8a8_adaln(const void* x, const void* scale, const void* shift, void* out, i
                int64_t scale_group, int64_t shift_group, double eps, int dtype, int rms,
                hipStream_t stream);
 
+/* modulated_norm fused with the per-token quantizer, for a norm whose only
+ * consumer is an INT8 linear (the DiT's norm1 -> QKV and norm2 -> FFN-up):
+ * no counterpart in the reference, which runs modulated_norm
+ * (inference/src/models/qwen_image21/numeric.rs:63-107, two "adaln" calls)
+ * and then quantizes its output inside int8_linear.  x [batch * tokens, d];
+ * row b * tokens + t uses scale0 / shift0 row b ([batch, d]) for t < prefix,
+ * else scale1 / shift1.  The codes q [rows, d] and row scales xs [rows] are
+ * those w8a8_quantize_rowwise gives for w8a8_adaln's output, bit for bit.
+ * Needs 16-byte aligned operands, d a multiple of 16 bytes / element size
+ * and at most 2048 16-byte chunks per row (else W8A8_ERR_VALUE: run the two
+ * steps).  Flags: W8A8_SCALE_RECIP. */
+int w8a8_modulated_norm_quant(const void* x, const void* scale0, const void* scale1, const void* shift0,
+                              const void* shift1, int8_t* q, float* xs, int64_t batch, int64_t tokens, int64_t d,
+                              int64_t prefix, double eps, int dtype, int rms, uint32_t flags, hipStream_t stream);
+
 /* Gated residual of the DiT block (inference/src/models/qwen_image21/
  * numeric.rs:110-125): x, y [batch, tokens, d], gates [batch, d];
  *   out[b, t] = T( fp32( x[b, t] + y[b, t] * gate[b] ) ),

@@ -122,6 +122,12 @@ def test_c_entries_reject_bad_arguments():
     assert lib.w8a8_adaln(None, None, None, None, 4, 8, 1, 1, 1e-6, _lib.BF16, 0, None) == _lib.ERR_VALUE
     assert lib.w8a8_adaln(None, None, None, None, 4, 8, 1, 1, 1e-6, 7, 0, None) == _lib.ERR_RUNTIME
     assert lib.w8a8_adaln(None, None, None, None, 0, 8, 1, 1, 1e-6, _lib.BF16, 0, None) == _lib.OK
+    assert lib.w8a8_modulated_norm_quant(None, None, None, None, None, None, None, 2, 3, 0, 0, 1e-6, _lib.BF16, 0, 0,
+                                         None) == _lib.ERR_VALUE
+    assert lib.w8a8_modulated_norm_quant(None, None, None, None, None, None, None, 2, 3, 8, 0, 1e-6, _lib.BF16, 0, 0,
+                                         None) == _lib.ERR_VALUE
+    assert lib.w8a8_modulated_norm_quant(None, None, None, None, None, None, None, 0, 3, 8, 0, 1e-6, _lib.BF16, 0, 0,
+                                         None) == _lib.OK
     assert lib.w8a8_gated_residual(None, None, None, None, None, 2, 3, 8, 0, _lib.BF16, None) == _lib.ERR_VALUE
     assert lib.w8a8_gated_residual(None, None, None, None, None, 0, 3, 8, 0, _lib.BF16, None) == _lib.OK
     assert lib.w8a8_quantize_rowwise_modulated(None, _lib.BF16, None, None, None, 2, 8, 0, None) == _lib.ERR_VALUE

@@ -160,3 +160,36 @@ def test_glue_full_size_sampled_rows():
     W.gated_residual(xd, y.to(DEV), (g0.to(DEV), g1.to(DEV)), P)
     want = E.gated_residual(xs.clone(), y[:, rows], (g0, g1), pref)
     assert np.array_equal(storage(xd[:, rows.to(DEV)], "bf16"), storage(want, "bf16"))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("rms", [False, True])
+@pytest.mark.parametrize("prefix", [0, 256])
+def test_modulated_norm_quant_equals_norm_then_quantizer(dtype, rms, prefix):
+    """The fused norm + quantizer against the two library steps it replaces
+    (adaLN with the text prefix, then the per-token quantizer): codes and
+    row scales bit for bit."""
+    g = torch.Generator().manual_seed(48 + prefix)
+    x = (torch.randn(2, 700, 3072, generator=g) * 1.5 + 0.2).to(TD[dtype])
+    s0, s1 = ((torch.randn(2, 1, 3072, generator=g) * 0.4).to(TD[dtype]) for _ in range(2))
+    shift = (torch.randn(2, 1, 3072, generator=g) * 0.1).to(TD[dtype])
+    xd = x.to(DEV)
+    sc = (s0.to(DEV), s1.to(DEV))
+    q, s = W.modulated_norm_quant(xd, sc, prefix, shift.to(DEV), 1e-6, rms=rms)
+    n = W.modulated_norm(xd, sc, prefix, shift.to(DEV), 1e-6, rms=rms)
+    q2, s2 = W.quantize_rowwise(n.reshape(-1, 3072))
+    assert torch.equal(q, q2)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s2.cpu().numpy().view(np.uint32))
+
+
+def test_modulated_norm_quant_odd_width_and_fallback():
+    """A width of 1000 (125 chunks, fused kernel) and an unaligned width of 1001
+    (two-step fallback), both equal to norm-then-quantize."""
+    for d in (1000, 1001):
+        g = torch.Generator().manual_seed(49 + d)
+        x = torch.randn(1, 33, d, generator=g).to(torch.bfloat16).to(DEV)
+        s0, s1 = ((torch.randn(1, 1, d, generator=g) * 0.3).to(torch.bfloat16).to(DEV) for _ in range(2))
+        zero = torch.zeros(1, 1, d, dtype=torch.bfloat16, device=DEV)
+        q, s = W.modulated_norm_quant(x, (s0, s1), 5, zero, 1e-6)
+        q2, s2 = W.quantize_rowwise(W.modulated_norm(x, (s0, s1), 5, zero, 1e-6).reshape(-1, d))
+        assert torch.equal(q, q2) and torch.equal(s, s2)
