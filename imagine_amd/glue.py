@@ -15,7 +15,7 @@ slices.
 import torch
 
 from . import _lib
-from .ops import _bias, _dtype_code, _ptr, _require_cuda, _stream, _weight_scale, route
+from .ops import _bias, _dtype_code, _ptr, _require_cuda, _stream, _weight_scale, quantize_rowwise, route
 
 
 def _modulation(t, x, n, d):
@@ -177,7 +177,6 @@ def modulated_norm_quant(x, scale, prefix, shift, eps, rms=False, *, scale_form=
     One kernel when the rows fit its register layout (16-byte aligned, at most
     2048 16-byte chunks), else those two steps.  ``shift`` is the one shift
     tensor of both token ranges, as the reference's ``zero``."""
-    from .ops import quantize_rowwise
     _require_cuda(x, *scale, shift)
     if x.dim() != 3:
         raise RuntimeError("modulated_norm_quant: x must be [batch, tokens, d]")
