@@ -14,10 +14,11 @@
 //                       then the per-token quantizer on xm, in one kernel.
 //
 // All three are bandwidth kernels over bf16/fp16/fp32 rows, fp32 arithmetic.
-// adaln: one 256-thread block per row; aligned rows of up to 2048 16-byte
-// chunks stay in registers (CPL chunks per lane) between the reduction passes
-// and the output pass, so x is read once; other rows take a generic kernel
-// that re-reads the row.  Gated residual: 16-byte chunks, grid-stride.
+// adaln: one block per row (128 threads up to 1024 16-byte chunks, else
+// 256); aligned rows of up to 2048 chunks stay in registers (CPL chunks per
+// lane) between the reduction passes and the output pass, so x is read once;
+// other rows take a generic kernel that re-reads the row.  Gated residual:
+// 16-byte chunks, grid-stride.
 #include <algorithm>
 
 #include "w8a8_common.h"
@@ -27,6 +28,20 @@ namespace w8a8 {
 namespace {
 
 constexpr int kGlueThreads = 256;
+
+// Sum over a block of NW waves (part: NW floats of LDS).
+template <int NW>
+__device__ __forceinline__ float block_sum_w(float v, float* part) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    __syncthreads();   // earlier readers of part are done
+    if ((threadIdx.x % kWave) == 0) part[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float s = part[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) s += part[w];
+    return s;
+}
 
 __device__ __forceinline__ float block_sum(float v, float* part) {
 #pragma unroll
@@ -89,15 +104,16 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows(const void* __restric
 // Register-resident adaln: lane chunk c = tid + j * 256 of the row (E values
 // per 16-byte chunk); same operations per element as adaln_rows, so the same
 // results up to the order of the fp32 row sums.
-template <int DT, bool RMS, int CPL>
-__global__ __launch_bounds__(kGlueThreads) void adaln_rows_vec(const void* __restrict__ x,
+template <int DT, bool RMS, int CPL, int NT>
+__global__ __launch_bounds__(NT) void adaln_rows_vec(const void* __restrict__ x,
                                                                const void* __restrict__ scale,
                                                                const void* __restrict__ shift,
                                                                void* __restrict__ out, int64_t d,
                                                                int64_t sg, int64_t tg, float eps) {
     using D = DType<DT>;
     constexpr int E = 16 / D::bytes;
-    __shared__ float part[4];
+    constexpr int NW = NT / kWave;
+    __shared__ float part[NW];
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
     const int64_t nchunks = d / E;
@@ -108,7 +124,7 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows_vec(const void* __res
     uint4 raw[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        const int64_t c = tid + static_cast<int64_t>(j) * NT;
         raw[j] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
     }
     auto elem = [&](const uint4& v, int i) {
@@ -125,7 +141,7 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows_vec(const void* __res
                 const float v = elem(raw[j], i);
                 s2 = fmaf(v, v, s2);
             }
-        s2 = block_sum(s2, part);
+        s2 = block_sum_w<NW>(s2, part);
         rstd = 1.0f / sqrtf(s2 * inv_d + eps);
     } else {
         float s1 = 0.0f;
@@ -133,11 +149,11 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows_vec(const void* __res
         for (int j = 0; j < CPL; ++j)
 #pragma unroll
             for (int i = 0; i < E; ++i) s1 += elem(raw[j], i);
-        mean = block_sum(s1, part) * inv_d;
+        mean = block_sum_w<NW>(s1, part) * inv_d;
         float s2 = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+            const int64_t c = tid + static_cast<int64_t>(j) * NT;
             if (c >= nchunks) break;   // padding chunks are zeros, not row values
 #pragma unroll
             for (int i = 0; i < E; ++i) {
@@ -145,13 +161,13 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows_vec(const void* __res
                 s2 = fmaf(cv, cv, s2);
             }
         }
-        const float var = block_sum(s2, part) * inv_d;
+        const float var = block_sum_w<NW>(s2, part) * inv_d;
         rstd = 1.0f / sqrtf(fmaxf(var, 0.0f) + eps);
     }
     const float bias = -rstd * mean;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        const int64_t c = tid + static_cast<int64_t>(j) * NT;
         if (c >= nchunks) break;
         const uint4 sv = sr[c], hv = hr[c];
         uint4 res;
@@ -175,15 +191,16 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows_vec(const void* __res
 // one launch); its T outputs, computed exactly as adaln_rows_vec computes
 // them, replace the raw row in registers, and their codes and row scale are
 // those the quantizer gives for the stored output.
-template <int DT, bool RMS, int CPL>
-__global__ __launch_bounds__(kGlueThreads) void modnorm_quant_rows_vec(
+template <int DT, bool RMS, int CPL, int NT>
+__global__ __launch_bounds__(NT) void modnorm_quant_rows_vec(
     const void* __restrict__ x, const void* __restrict__ scale0, const void* __restrict__ scale1,
     const void* __restrict__ shift0, const void* __restrict__ shift1, int8_t* __restrict__ q,
     float* __restrict__ xs, int64_t tokens, int64_t d, int64_t prefix, float eps, int recip) {
     using D = DType<DT>;
     using OS = typename D::storage;
     constexpr int E = 16 / D::bytes;
-    __shared__ float part[4];
+    constexpr int NW = NT / kWave;
+    __shared__ float part[NW];
     const int64_t row = blockIdx.x;
     const int64_t b = row / tokens, t = row % tokens;
     const int tid = threadIdx.x;
@@ -196,7 +213,7 @@ __global__ __launch_bounds__(kGlueThreads) void modnorm_quant_rows_vec(
     uint4 raw[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        const int64_t c = tid + static_cast<int64_t>(j) * NT;
         raw[j] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
     }
     auto elem = [&](const uint4& v, int i) { return D::load(reinterpret_cast<const OS*>(&v)[i]); };
@@ -211,7 +228,7 @@ __global__ __launch_bounds__(kGlueThreads) void modnorm_quant_rows_vec(
                 const float v = elem(raw[j], i);
                 s2 = fmaf(v, v, s2);
             }
-        s2 = block_sum(s2, part);
+        s2 = block_sum_w<NW>(s2, part);
         rstd = 1.0f / sqrtf(s2 * inv_d + eps);
     } else {
         float s1 = 0.0f;
@@ -219,11 +236,11 @@ __global__ __launch_bounds__(kGlueThreads) void modnorm_quant_rows_vec(
         for (int j = 0; j < CPL; ++j)
 #pragma unroll
             for (int i = 0; i < E; ++i) s1 += elem(raw[j], i);
-        mean = block_sum(s1, part) * inv_d;
+        mean = block_sum_w<NW>(s1, part) * inv_d;
         float s2 = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+            const int64_t c = tid + static_cast<int64_t>(j) * NT;
             if (c >= nchunks) break;
 #pragma unroll
             for (int i = 0; i < E; ++i) {
@@ -231,14 +248,14 @@ __global__ __launch_bounds__(kGlueThreads) void modnorm_quant_rows_vec(
                 s2 = fmaf(cv, cv, s2);
             }
         }
-        const float var = block_sum(s2, part) * inv_d;
+        const float var = block_sum_w<NW>(s2, part) * inv_d;
         rstd = 1.0f / sqrtf(fmaxf(var, 0.0f) + eps);
     }
     const float bias = -rstd * mean;
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        const int64_t c = tid + static_cast<int64_t>(j) * NT;
         if (c >= nchunks) break;
         const uint4 sv = sr[c], hv = hr[c];
         OS* rp = reinterpret_cast<OS*>(&raw[j]);
@@ -256,14 +273,16 @@ __global__ __launch_bounds__(kGlueThreads) void modnorm_quant_rows_vec(
     __syncthreads();   // block_sum's readers of part are done
     if ((tid % kWave) == 0) part[tid / kWave] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    amax = part[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) amax = fmaxf(amax, part[w]);
     const float s = row_scale<DT>(amax, recip != 0);
     if (tid == 0) xs[row] = s;
     const RowQuant rq = row_quant<DT>(s);
     int8_t* qr = q + row * d;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const int64_t c = tid + static_cast<int64_t>(j) * kGlueThreads;
+        const int64_t c = tid + static_cast<int64_t>(j) * NT;
         if (c >= nchunks) break;
         if constexpr (E == 8) {
             uint2 packed;
@@ -362,11 +381,18 @@ __global__ __launch_bounds__(kGlueThreads) void quant_rows_modulated(const void*
 
 namespace {
 
+// Rows of up to 1024 16-byte chunks take 128 threads (2 waves), longer rows
+// 256: at the DiT width (3072 bf16 = 384 chunks) every lane then holds 3
+// chunks, where 256 threads would leave a quarter of them idle.
 template <int DT, bool RMS, int CPL>
 void launch_adaln_vec(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
-                      int64_t sg, int64_t tg, float eps, hipStream_t stream) {
-    hipLaunchKernelGGL((adaln_rows_vec<DT, RMS, CPL>), dim3(static_cast<unsigned>(n)), dim3(kGlueThreads), 0,
-                       stream, x, scale, shift, out, d, sg, tg, eps);
+                      int64_t sg, int64_t tg, float eps, bool narrow, hipStream_t stream) {
+    if (narrow)
+        hipLaunchKernelGGL((adaln_rows_vec<DT, RMS, CPL, 128>), dim3(static_cast<unsigned>(n)), dim3(128), 0,
+                           stream, x, scale, shift, out, d, sg, tg, eps);
+    else
+        hipLaunchKernelGGL((adaln_rows_vec<DT, RMS, CPL, 256>), dim3(static_cast<unsigned>(n)), dim3(256), 0,
+                           stream, x, scale, shift, out, d, sg, tg, eps);
 }
 
 template <int DT, bool RMS>
@@ -375,16 +401,18 @@ bool adaln_vec_dispatch(const void* x, const void* scale, const void* shift, voi
     constexpr int E = 16 / DType<DT>::bytes;
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (d % E != 0 || !al(x) || !al(scale) || !al(shift) || !al(out)) return false;
-    const int64_t per_lane = (d / E + kGlueThreads - 1) / kGlueThreads;
+    const bool narrow = d / E <= 1024;
+    const int nt = narrow ? 128 : 256;
+    const int64_t per_lane = (d / E + nt - 1) / nt;
     switch (per_lane) {
-        case 1: launch_adaln_vec<DT, RMS, 1>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
-        case 2: launch_adaln_vec<DT, RMS, 2>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
-        case 3: launch_adaln_vec<DT, RMS, 3>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
-        case 4: launch_adaln_vec<DT, RMS, 4>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        case 1: launch_adaln_vec<DT, RMS, 1>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 2: launch_adaln_vec<DT, RMS, 2>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 3: launch_adaln_vec<DT, RMS, 3>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 4: launch_adaln_vec<DT, RMS, 4>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
         case 5:
-        case 6: launch_adaln_vec<DT, RMS, 6>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        case 6: launch_adaln_vec<DT, RMS, 6>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
         case 7:
-        case 8: launch_adaln_vec<DT, RMS, 8>(x, scale, shift, out, n, d, sg, tg, eps, stream); return true;
+        case 8: launch_adaln_vec<DT, RMS, 8>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
         default: return false;
     }
 }
@@ -401,9 +429,17 @@ bool modnorm_quant_dispatch(const void* x, const void* s0, const void* s1, const
     auto al = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (d % E != 0 || !al(x) || !al(s0) || !al(s1) || !al(h0) || !al(h1) || reinterpret_cast<uintptr_t>(q) % E != 0)
         return false;
-    const int64_t per_lane = (d / E + kGlueThreads - 1) / kGlueThreads;
-    const dim3 grid(static_cast<unsigned>(rows)), block(kGlueThreads);
-#define W8A8_MNQ(CPL) hipLaunchKernelGGL((modnorm_quant_rows_vec<DT, RMS, CPL>), grid, block, 0, stream, x, s0, s1, h0, h1, q, xs, tokens, d, prefix, eps, recip)
+    const bool narrow = d / E <= 1024;   // 128 threads per row, as launch_adaln_vec
+    const int nt = narrow ? 128 : 256;
+    const int64_t per_lane = (d / E + nt - 1) / nt;
+    const dim3 grid(static_cast<unsigned>(rows)), block(nt);
+#define W8A8_MNQ(CPL)                                                                                     \
+    do {                                                                                                  \
+        if (narrow)                                                                                       \
+            hipLaunchKernelGGL((modnorm_quant_rows_vec<DT, RMS, CPL, 128>), grid, block, 0, stream, x, s0, s1, h0, h1, q, xs, tokens, d, prefix, eps, recip); \
+        else                                                                                              \
+            hipLaunchKernelGGL((modnorm_quant_rows_vec<DT, RMS, CPL, 256>), grid, block, 0, stream, x, s0, s1, h0, h1, q, xs, tokens, d, prefix, eps, recip); \
+    } while (0)
     switch (per_lane) {
         case 1: W8A8_MNQ(1); return true;
         case 2: W8A8_MNQ(2); return true;
