@@ -12,6 +12,7 @@
 // exchange for 4-wave rows), and the int8 codes leave as 64-bit stores.
 // Rows that do not fit, or unaligned operands, take the generic kernel.
 #include <algorithm>
+#include <cstdlib>
 
 #include "w8a8_common.h"
 
@@ -173,10 +174,19 @@ static void launch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t K
                        xs, M, K, recip);
 }
 
-// Rows of up to 128 chunks take one wave each; longer rows four waves, which
-// keeps more waves streaming per row (K = 3072 bf16: 23.5 us with 4 waves of 2
-// chunks per lane against 26.1 us with one wave of 6; a plain copy of the same
-// bytes takes 21.8 us).
+// Rows of up to 128 chunks take one wave each; longer rows two or four waves,
+// which keeps more waves streaming per row (K = 3072 bf16, 384 chunks: two
+// waves of 3 chunks per lane, every lane busy, ~23.3 us; four waves of 2,
+// ~24.6 us; one wave of 6, 26.1 us; a plain copy of the same bytes 21.8 us).
+// W8A8_QUANT_ROWS=4 keeps rows of 257..384 chunks on 4 waves (tuning knob).
+static bool quant_two_wave_rows() {
+    static const bool on = [] {
+        const char* e = std::getenv("W8A8_QUANT_ROWS");
+        return !(e && e[0] == '4');
+    }();
+    return on;
+}
+
 template <int DT, bool GELU, bool SO>
 static bool dispatch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, int recip,
                          hipStream_t stream) {
@@ -185,6 +195,7 @@ static bool dispatch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t
     if (nchunks <= 64) launch_vec<DT, 1, 1, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 128) launch_vec<DT, 1, 2, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 256) launch_vec<DT, 4, 1, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 384 && quant_two_wave_rows()) launch_vec<DT, 2, 3, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 512) launch_vec<DT, 4, 2, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 768) launch_vec<DT, 4, 3, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 1024) launch_vec<DT, 4, 4, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
