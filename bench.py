@@ -390,8 +390,9 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
     random-init int8 weights (60 distinct sets, ~6.8 GB, resident in HBM).
     Per block, as the reference's block forward (models/qwen_image21/dit.rs:
     285-340): text and image modulation GEMVs (M=2, N=18432) -> norm1
-    (modulated_norm, text prefix 256) -> QKV -> QK RMSNorm + RoPE (torch bf16)
-    -> attention (torch fused SDPA; no math fallback) -> out-proj -> gated
+    (modulated_norm, text prefix 256) -> QKV -> QK RMSNorm + RoPE
+    (imagine_amd.rms_rope; a 1D frequency table stands in for the 2D one) ->
+    attention (torch fused SDPA; no math fallback) -> out-proj -> gated
     residual -> norm2 -> FFN-up -> FFN-down with input_act gelu_tanh -> gated
     residual.  norm1 and norm2 only feed QKV and FFN-up, so they run as the
     fused norm + quantizer (modulated_norm_quant, the same codes as norm then
@@ -421,8 +422,8 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
     x0 = torch.randn(B, T, D, device=dev, generator=g).to(bf)
     inv = 1.0 / (10000.0 ** (torch.arange(0, HD, 2, device=dev).float() / HD))
     ang = torch.arange(T, device=dev).float()[:, None] * inv[None]
-    cos = ang.cos().to(bf)[None, :, None, :]
-    sin = ang.sin().to(bf)[None, :, None, :]
+    c_, s_ = ang.cos(), ang.sin()
+    freqs = torch.stack([torch.stack([c_, -s_], -1), torch.stack([s_, c_], -1)], -2)[None, :, None].contiguous()
     zero = torch.zeros(B, 1, D, device=dev, dtype=bf)
     ev = {"w8a8": [], "glue": [], "norm_quant": []}
 
@@ -434,18 +435,13 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
         ev[kind].append((s, e))
         return r
 
-    def rope(t):
-        t1, t2 = t[..., 0::2], t[..., 1::2]
-        return torch.stack((t1 * cos - t2 * sin, t1 * sin + t2 * cos), dim=-1).flatten(-2)
-
     def block(x, p):
         mt = [c.reshape(B, 1, D).contiguous() for c in timed("w8a8", W.int8_linear, temb, *p["mod_txt"]).chunk(6, -1)]
         mi = [c.reshape(B, 1, D).contiguous() for c in timed("w8a8", W.int8_linear, temb, *p["mod_img"]).chunk(6, -1)]
         q1, s1 = timed("norm_quant", W.modulated_norm_quant, x, (mt[1], mi[1]), T_txt, zero, 1e-6)
         qkv = timed("w8a8", W.gemm_dequant, q1, p["qkv"][0], s1, *p["qkv"][1:], torch.bfloat16)
         qkv = qkv.view(B, T, 3, H, HD)
-        q = rope(torch.nn.functional.rms_norm(qkv[:, :, 0], (HD,), p["qn"], 1e-6))
-        k = rope(torch.nn.functional.rms_norm(qkv[:, :, 1], (HD,), p["kn"], 1e-6))
+        q, k = timed("glue", W.rms_rope, qkv[:, :, 0], qkv[:, :, 1], freqs, p["qn"], p["kn"], 1e-6)
         v = qkv[:, :, 2]
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             o = torch.nn.functional.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2),
@@ -487,7 +483,7 @@ def measure_dit_step(W, dev, steps=2, warmup=1, blocks=60):
             "glue_share": round(gl / ms, 3), "norm_quant_ms": round(nq, 2), "norm_quant_share": round(nq / ms, 3),
             "blocks": blocks, "M": B * T, "steps": steps,
             "output_finite": finite,
-            "rest": "QK RMSNorm, RoPE and attention (fused SDPA) in torch bf16"}
+            "rest": "attention (torch fused SDPA) and the head split / merge copies"}
 
 
 def run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs):

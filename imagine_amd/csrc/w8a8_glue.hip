@@ -9,6 +9,7 @@
 //   gated residual      x += y * gate, tokens before the prefix with gate0,
 //                       the rest with gate1 (models/qwen_image21/numeric.rs:
 //                       110-125, ATen addcmul_: T(fp32(x + y * g))).
+//   rms_rope            the attention's QK RMSNorm + RoPE (backend_rope.rs:204-222).
 //   modulated quantizer the batch-one modulation of int8_linear_modulated
 //                       (backend_bindings.rs:329-405): xm = T(x * T(1 + s_k)),
 //                       then the per-token quantizer on xm, in one kernel.
@@ -296,6 +297,62 @@ __global__ __launch_bounds__(NT) void modnorm_quant_rows_vec(
     }
 }
 
+// QK RMSNorm + RoPE of the attention (Kitchen's rms_rope as the crate's eager
+// route computes it, backend_rope.rs:204-222 and :146-159, non-split, full
+// rotation): for each [head_dim] row of q and of k,
+//   m = T(x * rsqrt(mean(x^2) + eps) * scale)   (aten rms_norm with weight: fp32, one rounding)
+//   out[2i + j] = T( f[i][j][0] * m[2i] + f[i][j][1] * m[2i + 1] )   (fp32 products and sum)
+// with f the row's [d/2][2][2] fp32 rotation from freqs [freq_batch, seq, d/2, 2, 2].
+// One wave per row: lane l holds the rotation pairs l + 64 j (PPL pairs per
+// lane), so the row's sum of squares is one wave butterfly.  q rows come
+// first, then k rows; rows are [batch, seq, heads] in order.
+template <int DT, int PPL>
+__global__ __launch_bounds__(256) void rms_rope_rows(const void* __restrict__ q, const void* __restrict__ k,
+                                                     const float* __restrict__ freqs,
+                                                     const void* __restrict__ q_scale,
+                                                     const void* __restrict__ k_scale, void* __restrict__ q_out,
+                                                     void* __restrict__ k_out, int64_t rows, int64_t seq,
+                                                     int64_t heads, int64_t d, int freq_per_batch, float eps) {
+    using D = DType<DT>;
+    using OS = typename D::storage;
+    const int lane = threadIdx.x % kWave;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+    if (wave >= 2 * rows) return;   // whole waves only; the kernel has no block barrier
+    const bool is_k = wave >= rows;
+    const int64_t row = is_k ? wave - rows : wave;
+    const OS* x = static_cast<const OS*>(is_k ? k : q) + row * d;
+    const OS* w = static_cast<const OS*>(is_k ? k_scale : q_scale);
+    OS* o = static_cast<OS*>(is_k ? k_out : q_out) + row * d;
+    const int64_t b = row / (seq * heads), t = (row / heads) % seq;
+    const float* f = freqs + ((freq_per_batch ? b * seq : 0) + t) * (d / 2) * 4;
+    float a[PPL], c[PPL];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+        const int64_t p = lane + j * kWave;
+        a[j] = c[j] = 0.0f;
+        if (2 * p < d) {
+            a[j] = D::load(x[2 * p]);
+            c[j] = D::load(x[2 * p + 1]);
+        }
+        sum += a[j] * a[j];
+        sum += c[j] * c[j];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    const float r = 1.0f / sqrtf(sum * (1.0f / static_cast<float>(d)) + eps);
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+        const int64_t p = lane + j * kWave;
+        if (2 * p >= d) break;
+        const float m0 = D::round(a[j] * r * D::load(w[2 * p]));
+        const float m1 = D::round(c[j] * r * D::load(w[2 * p + 1]));
+        const float4 fv = reinterpret_cast<const float4*>(f)[p];   // f[p][0][0], f[p][0][1], f[p][1][0], f[p][1][1]
+        o[2 * p] = D::store(fv.x * m0 + fv.y * m1);
+        o[2 * p + 1] = D::store(fv.z * m0 + fv.w * m1);
+    }
+}
+
 // x[b, t, :] += y[b, t, :] * gate[b, :], gate = gate0 for t < prefix else gate1;
 // gates are [batch, d].  out may alias x (the reference updates x in place).
 template <int DT>
@@ -524,6 +581,22 @@ void launch_gated_residual(const void* x, const void* y, const void* gate0, cons
             hipLaunchKernelGGL((gated_residual_rows<W8A8_F32>), grid, block, 0, stream, x, y, gate0, gate1, out, tokens, d, prefix);
             break;
     }
+}
+
+bool launch_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
+                     void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
+                     bool freq_per_batch, float eps, int dtype, hipStream_t stream) {
+    const int64_t rows = batch * seq * heads;
+    const dim3 grid(static_cast<unsigned>((2 * rows + 3) / 4)), block(256);
+    const int fpb = freq_per_batch ? 1 : 0;
+#define W8A8_RR(DT, PPL) hipLaunchKernelGGL((rms_rope_rows<DT, PPL>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, rows, seq, heads, d, fpb, eps)
+    const int ppl = d <= 128 ? 1 : d <= 256 ? 2 : 0;
+    if (ppl == 0) return false;
+    if (dtype == W8A8_BF16) { if (ppl == 1) W8A8_RR(W8A8_BF16, 1); else W8A8_RR(W8A8_BF16, 2); }
+    else if (dtype == W8A8_F16) { if (ppl == 1) W8A8_RR(W8A8_F16, 1); else W8A8_RR(W8A8_F16, 2); }
+    else { if (ppl == 1) W8A8_RR(W8A8_F32, 1); else W8A8_RR(W8A8_F32, 2); }
+#undef W8A8_RR
+    return true;
 }
 
 void launch_quant_modulated(const void* x, int dtype, const void* mod, int8_t* q, float* xs, int64_t M,

@@ -198,3 +198,31 @@ def modulated_norm_quant(x, scale, prefix, shift, eps, rms=False, *, scale_form=
         _dtype_code(x.dtype, "adaln"), 1 if rms else 0, _lib.SCALE_RECIP if scale_form == "recip" else 0,
         _stream(x.device)))
     return q, s
+
+
+def rms_rope(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6):
+    """Kitchen's ``rms_rope`` (backend_rope.rs:364-440, the eager numerics of
+    eager_rms :204-222 / eager_apply :146-159, non-split): RMSNorm of every
+    head row of q and k with its weight, then the pairwise rotation by
+    ``freqs_cis``.  q, k [B, S, H, D]; freqs_cis fp32 [B|1, S, 1, D/2, 2, 2]
+    (the DiT's layout); scales [D].  Returns (q_out, k_out)."""
+    _require_cuda(q, k, freqs_cis, q_scale)
+    k_scale = q_scale if k_scale is None else k_scale
+    if q.dim() != 4 or k.shape != q.shape:
+        raise RuntimeError("rms_rope: q and k must be [batch, seq, heads, head_dim] of one shape")
+    b, s, h, d = q.shape
+    if freqs_cis.dtype != torch.float32:
+        raise NotImplementedError("rms_rope: freqs_cis in a dtype other than float32 is not part of this build")
+    fs = tuple(freqs_cis.shape)
+    if len(fs) != 6 or fs[0] not in (1, b) or fs[1] != s or fs[2] != 1 or fs[3:] != (d // 2, 2, 2):
+        raise NotImplementedError(f"rms_rope: freqs_cis layout {fs} is not part of this build")
+    if any(t.dtype != q.dtype for t in (k, q_scale, k_scale)):
+        raise RuntimeError("rms_rope: k and the scales must have the dtype of q")
+    q, k = q.contiguous(), k.contiguous()
+    f = freqs_cis.contiguous()
+    qs, ks = q_scale.reshape(-1).contiguous(), k_scale.reshape(-1).contiguous()
+    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    _lib.check(_lib.load().w8a8_rms_rope(
+        _ptr(q), _ptr(k), _ptr(f), _ptr(qs), _ptr(ks), _ptr(qo), _ptr(ko), b, s, h, d, 1 if fs[0] == b and b > 1 else 0,
+        float(epsilon), _dtype_code(q.dtype, "rms_rope"), _stream(q.device)))
+    return qo, ko

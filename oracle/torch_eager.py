@@ -107,3 +107,21 @@ def modulate(x, modulation_scale):
     width = x.shape[-1]
     shape = [1] * (x.dim() - 1) + [width]
     return x.mul(modulation_scale.reshape(shape).add(1.0))
+
+
+def rope_apply(x, f):
+    """backend_rope.rs:146-159 (eager_apply, non-split): x in f's dtype viewed
+    as pairs, out[2i + j] = f[i][j][0] x[2i] + f[i][j][1] x[2i + 1] (mul, then
+    addcmul_), back to x's dtype."""
+    shape = x.shape
+    inp = x.to(f.dtype).reshape(*shape[:-1], -1, 1, 2)
+    out = f[..., 0] * inp[..., 0]
+    out.addcmul_(f[..., 1], inp[..., 1])
+    return out.reshape(shape).to(x.dtype)
+
+
+def rms_rope(q, k, freqs_cis, q_scale, k_scale, eps):
+    """backend_rope.rs:204-222 (eager_rms, whole head rotated) on q and k."""
+    def one(x, s):
+        return rope_apply(torch.nn.functional.rms_norm(x, (x.shape[-1],), s, eps), freqs_cis)
+    return one(q, q_scale), one(k, k_scale)

@@ -135,3 +135,56 @@ def test_c_entries_reject_bad_arguments():
                                                None) == _lib.ERR_VALUE
     assert lib.w8a8_int8_linear_modulated(None, _lib.BF16, None, None, None, 1, None, None, _lib.BF16, 2, 4, 8,
                                           _lib.FUSED_QUANT, None, 0, None) == _lib.ERR_VALUE
+
+
+def test_rope_apply_oracle_is_the_complex_rotation():
+    """The eager rotation on fp32 pairs equals the complex product
+    (x0 + i x1)(cos + i sin) in float64 to fp32 rounding, is the identity for
+    zero angles, and keeps every pair's length."""
+    g = torch.Generator().manual_seed(51)
+    x = torch.randn(2, 7, 3, 16, generator=g)
+    theta = torch.rand(7, 8, generator=g, dtype=torch.float64) * 6.3
+    c, s = theta.cos(), theta.sin()
+    f = torch.stack([torch.stack([c, -s], -1), torch.stack([s, c], -1)], -2).float()[None, :, None]  # [1,7,1,8,2,2]
+    out = E.rope_apply(x, f).double()
+    z = torch.complex(x[..., 0::2].double(), x[..., 1::2].double()) * torch.complex(c, s)[None, :, None]
+    assert torch.allclose(out[..., 0::2], z.real, rtol=0, atol=1e-5)
+    assert torch.allclose(out[..., 1::2], z.imag, rtol=0, atol=1e-5)
+    ident = torch.zeros(1, 7, 1, 8, 2, 2)
+    ident[..., 0, 0] = 1
+    ident[..., 1, 1] = 1
+    assert torch.equal(E.rope_apply(x, ident), x)
+    n_in = x[..., 0::2] ** 2 + x[..., 1::2] ** 2
+    n_out = out[..., 0::2] ** 2 + out[..., 1::2] ** 2
+    assert torch.allclose(n_out, n_in.double(), rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_rms_norm_with_weight_rounds_once(dtype):
+    """ATen's rms_norm with a weight (what backend_rope.rs:216 calls) is
+    T(x * rsqrt(mean(x^2) + eps) * w) with the weight product in fp32 and one
+    rounding; rounding after the normalisation and again after the weight
+    disagrees on about a quarter of the bf16 outputs."""
+    g = torch.Generator().manual_seed(52)
+    x = torch.randn(64, 128, generator=g).to(TD[dtype])
+    w = (torch.randn(128, generator=g) * 0.5 + 1).to(TD[dtype])
+    got = torch.nn.functional.rms_norm(x, (128,), w, 1e-6)
+    xf = x.double()
+    r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    once = (xf * r * w.double()).to(TD[dtype])
+    twice = ((xf * r).to(TD[dtype]).double() * w.double()).to(TD[dtype])
+    assert (got == once).float().mean() > 0.99
+    assert (got == twice).float().mean() < 0.95
+
+
+def test_rms_rope_host_errors():
+    q = torch.zeros(1, 4, 2, 8, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        W.rms_rope(q, q, torch.zeros(1, 4, 1, 4, 2, 2), torch.ones(8, dtype=torch.bfloat16))   # CPU tensors
+    lib = _lib.load()
+    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 1, 4, 2, 7, 0, 1e-6, _lib.BF16,
+                             None) == _lib.ERR_VALUE
+    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 0, 4, 2, 8, 0, 1e-6, _lib.BF16,
+                             None) == _lib.OK
+    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 1, 4, 2, 8, 0, 1e-6, _lib.BF16,
+                             None) == _lib.ERR_VALUE

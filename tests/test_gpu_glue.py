@@ -193,3 +193,32 @@ def test_modulated_norm_quant_odd_width_and_fallback():
         q, s = W.modulated_norm_quant(x, (s0, s1), 5, zero, 1e-6)
         q2, s2 = W.quantize_rowwise(W.modulated_norm(x, (s0, s1), 5, zero, 1e-6).reshape(-1, d))
         assert torch.equal(q, q2) and torch.equal(s, s2)
+
+
+def _freqs(batch, seq, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    theta = torch.rand(batch, seq, d // 2, generator=g, dtype=torch.float64) * 50.0
+    c, s = theta.cos(), theta.sin()
+    return torch.stack([torch.stack([c, -s], -1), torch.stack([s, c], -1)], -2).float()[:, :, None]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("fb", [1, 2])
+def test_rms_rope_matches_eager_sequence(dtype, fb):
+    """QK RMSNorm + RoPE against the reference's eager sequence (rms_norm with
+    weight, then the fp32 pair rotation) on the CPU: two ulps of the rotated
+    pair's magnitude, and at least 97% of outputs bit-equal (the fp32 sum of
+    squares rounds in another order)."""
+    g = torch.Generator().manual_seed(52 + fb)
+    B, S, H, D = 2, 300, 24, 128
+    q = (torch.randn(B, S, H, D, generator=g) * 2).to(TD[dtype])
+    k = (torch.randn(B, S, H, D, generator=g) * 0.5).to(TD[dtype])
+    qs = (1 + 0.1 * torch.randn(D, generator=g)).to(TD[dtype])
+    ks = (1 + 0.1 * torch.randn(D, generator=g)).to(TD[dtype])
+    f = _freqs(fb, S, D, seed=53)
+    qo, ko = W.rms_rope(q.to(DEV), k.to(DEV), f.to(DEV), qs.to(DEV), ks.to(DEV), 1e-6)
+    wq, wk = E.rms_rope(q, k, f, qs, ks, 1e-6)
+    for got, want, x, s in ((qo, wq, q, qs), (ko, wk, k, ks)):
+        m = torch.nn.functional.rms_norm(x, (D,), s, 1e-6).float()
+        mag = (m[..., 0::2].abs() + m[..., 1::2].abs()).repeat_interleave(2, -1).numpy()
+        close(storage(got, dtype), storage(want, dtype), dtype, before_add=mag)
