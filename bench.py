@@ -358,6 +358,26 @@ def measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv):
                                         "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
                                         "bytes": per, "buffer_sets": nsets}
     del hx, ho
+    # QK RMSNorm + RoPE on q and k read in place out of the fused QKV output
+    # [2, 5856, 3, 24, 128] bf16, packed outputs; per launch: q and k read,
+    # q_out and k_out written, the fp32 [5856, 64, 2, 2] rotation table read
+    nh, hd = 24, HID // 24
+    per = 4 * hbytes + ht * (hd // 2) * 16
+    nsets = max(2, int(1.2e9 // (5 * hbytes)) + 1)
+    qkv = [torch.randn(hb, ht, 3, nh, hd, device=dev).to(torch.bfloat16) for _ in range(nsets)]
+    qo = [torch.empty(hb, ht, nh, hd, device=dev, dtype=torch.bfloat16) for _ in range(2 * nsets)]
+    fr = torch.randn(ht, hd // 2, 2, 2, device=dev)
+    sc = torch.ones(hd, device=dev, dtype=torch.bfloat16)
+    def rope(i):
+        j = i % nsets
+        W._lib.check(lib.w8a8_rms_rope(qkv[j].data_ptr(), qkv[j][:, :, 1].data_ptr(), fr.data_ptr(), sc.data_ptr(),
+                                       sc.data_ptr(), qo[2 * j].data_ptr(), qo[2 * j + 1].data_ptr(), hb, ht, nh, hd,
+                                       3 * nh * hd, 0, 1e-6, W._lib.BF16, stream()))
+    ms = median_of_batches(rope)
+    ex["rms_rope_qkv_2x5856x24x128"] = {"us": round(ms * 1e3, 2), "GB/s": round(per / (ms * 1e-3) / 1e9, 1),
+                                        "pct_hbm_peak": round(100 * per / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 1),
+                                        "bytes": per, "buffer_sets": nsets}
+    del qkv, qo
     # outlier workload: fused quant+GEMM vs unfused
     m, k, n = M_TOK, HID, FFN
     x = student_t(m, k, 3).to(dev)

@@ -44,7 +44,7 @@ void launch_quant_modulated(const void* x, int dtype, const void* mod, int8_t* q
                             int64_t K, int recip, hipStream_t stream);
 bool launch_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
                      void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
-                     bool freq_per_batch, float eps, int dtype, hipStream_t stream);
+                     int64_t x_stride, bool freq_per_batch, float eps, int dtype, hipStream_t stream);
 bool launch_modnorm_quant(const void* x, const void* s0, const void* s1, const void* h0, const void* h1, int8_t* q,
                           float* xs, int64_t rows, int64_t tokens, int64_t d, int64_t prefix, float eps, int dtype,
                           bool rms, int recip, hipStream_t stream);
@@ -173,16 +173,18 @@ int w8a8_modulated_norm_quant(const void* x, const void* scale0, const void* sca
 }
 
 int w8a8_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
-                  void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d, int freq_per_batch,
-                  double eps, int dtype, hipStream_t stream) {
+                  void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
+                  int64_t x_row_stride, int freq_per_batch, double eps, int dtype, hipStream_t stream) {
     if (batch < 0 || seq < 0 || heads < 0 || d < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
     if (!valid_dtype(dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported dtype for rms_rope");
     if (d % 2 != 0 || d > 256) return fail(W8A8_ERR_VALUE, "rms_rope needs an even head dimension of at most 256");
     if (batch == 0 || seq == 0 || heads == 0 || d == 0) return W8A8_OK;
+    if (x_row_stride < heads * d) return fail(W8A8_ERR_VALUE, "rms_rope: x_row_stride must be at least heads * d");
     if (!q || !k || !freqs || !q_scale || !k_scale || !q_out || !k_out) return fail(W8A8_ERR_VALUE, "null tensor pointer");
     if (reinterpret_cast<uintptr_t>(freqs) % 16 != 0) return fail(W8A8_ERR_VALUE, "freqs must be 16-byte aligned");
-    if (2 * batch * seq * heads > 0x7fffffffll * 4) return fail(W8A8_ERR_VALUE, "rms_rope: too many rows");
-    if (!w8a8::launch_rms_rope(q, k, freqs, q_scale, k_scale, q_out, k_out, batch, seq, heads, d, freq_per_batch != 0,
+    if (2 * batch * seq > 0x7fffffffll * 4) return fail(W8A8_ERR_VALUE, "rms_rope: too many tokens");
+    if (!w8a8::launch_rms_rope(q, k, freqs, q_scale, k_scale, q_out, k_out, batch, seq, heads, d, x_row_stride,
+                               freq_per_batch != 0,
                                static_cast<float>(eps), dtype, stream))
         return fail(W8A8_ERR_VALUE, "rms_rope needs an even head dimension of at most 256");
     return check_launch("rms_rope");

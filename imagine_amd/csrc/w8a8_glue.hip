@@ -302,54 +302,199 @@ __global__ __launch_bounds__(NT) void modnorm_quant_rows_vec(
 // rotation): for each [head_dim] row of q and of k,
 //   m = T(x * rsqrt(mean(x^2) + eps) * scale)   (aten rms_norm with weight: fp32, one rounding)
 //   out[2i + j] = T( f[i][j][0] * m[2i] + f[i][j][1] * m[2i + 1] )   (fp32 products and sum)
-// with f the row's [d/2][2][2] fp32 rotation from freqs [freq_batch, seq, d/2, 2, 2].
-// One wave per row: lane l holds the rotation pairs l + 64 j (PPL pairs per
-// lane), so the row's sum of squares is one wave butterfly.  q rows come
-// first, then k rows; rows are [batch, seq, heads] in order.
-template <int DT, int PPL>
-__global__ __launch_bounds__(256) void rms_rope_rows(const void* __restrict__ q, const void* __restrict__ k,
-                                                     const float* __restrict__ freqs,
-                                                     const void* __restrict__ q_scale,
-                                                     const void* __restrict__ k_scale, void* __restrict__ q_out,
-                                                     void* __restrict__ k_out, int64_t rows, int64_t seq,
-                                                     int64_t heads, int64_t d, int freq_per_batch, float eps) {
+// with f the token's [d/2][2][2] fp32 rotation from freqs [freq_batch, seq, d/2, 2, 2].
+// One wave per token of q or of k: lane l holds rotation pairs l + 64 j (PPL
+// pairs per lane) of the rotation row and both weights in registers for all
+// the token's heads, which it walks kHeadGroup at a time (independent row
+// sums, one wave butterfly each).  q tokens come first, then k tokens; tokens
+// are [batch, seq] in order.  Token (b, t) of q and k starts x_stride
+// elements after token (b, t - 1) (heads * d when packed, 3 * heads * d for
+// q / k read straight out of a fused QKV output), its heads d apart; the
+// outputs are packed [batch, seq, heads, d].  PAIR: every pair is read and
+// written as one 2-element access (row bases aligned to two elements).
+constexpr int kHeadGroup = 8;
+
+template <int DT, bool PAIR>
+__device__ __forceinline__ void load_pair(const typename DType<DT>::storage* x, int64_t i, float& a, float& c) {
+    using D = DType<DT>;
+    if constexpr (PAIR && DT == W8A8_F32) {
+        const float2 v = *reinterpret_cast<const float2*>(x + i);
+        a = v.x;
+        c = v.y;
+    } else if constexpr (PAIR) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(x + i);
+        a = D::load(static_cast<uint16_t>(v & 0xffffu));
+        c = D::load(static_cast<uint16_t>(v >> 16));
+    } else {
+        a = D::load(x[i]);
+        c = D::load(x[i + 1]);
+    }
+}
+
+template <int DT, bool PAIR>
+__device__ __forceinline__ void store_pair(typename DType<DT>::storage* o, int64_t i, float a, float c) {
+    using D = DType<DT>;
+    if constexpr (PAIR && DT == W8A8_F32) {
+        *reinterpret_cast<float2*>(o + i) = make_float2(a, c);
+    } else if constexpr (PAIR) {
+        *reinterpret_cast<uint32_t*>(o + i) =
+            static_cast<uint32_t>(D::store(a)) | (static_cast<uint32_t>(D::store(c)) << 16);
+    } else {
+        o[i] = D::store(a);
+        o[i + 1] = D::store(c);
+    }
+}
+
+template <int DT, int PPL, bool PAIR>
+__global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ q, const void* __restrict__ k,
+                                                       const float* __restrict__ freqs,
+                                                       const void* __restrict__ q_scale,
+                                                       const void* __restrict__ k_scale, void* __restrict__ q_out,
+                                                       void* __restrict__ k_out, int64_t tokens, int64_t seq,
+                                                       int64_t heads, int64_t d, int64_t x_stride,
+                                                       int freq_per_batch, float eps) {
     using D = DType<DT>;
     using OS = typename D::storage;
     const int lane = threadIdx.x % kWave;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
-    if (wave >= 2 * rows) return;   // whole waves only; the kernel has no block barrier
-    const bool is_k = wave >= rows;
-    const int64_t row = is_k ? wave - rows : wave;
-    const OS* x = static_cast<const OS*>(is_k ? k : q) + row * d;
+    if (wave >= 2 * tokens) return;   // whole waves only; the kernel has no block barrier
+    const bool is_k = wave >= tokens;
+    const int64_t tok = is_k ? wave - tokens : wave;
+    const OS* x = static_cast<const OS*>(is_k ? k : q) + tok * x_stride;
     const OS* w = static_cast<const OS*>(is_k ? k_scale : q_scale);
-    OS* o = static_cast<OS*>(is_k ? k_out : q_out) + row * d;
-    const int64_t b = row / (seq * heads), t = (row / heads) % seq;
-    const float* f = freqs + ((freq_per_batch ? b * seq : 0) + t) * (d / 2) * 4;
-    float a[PPL], c[PPL];
-    float sum = 0.0f;
+    OS* o = static_cast<OS*>(is_k ? k_out : q_out) + tok * heads * d;
+    const int64_t b = tok / seq, t = tok % seq;
+    const float4* f = reinterpret_cast<const float4*>(freqs + ((freq_per_batch ? b * seq : 0) + t) * (d / 2) * 4);
+    float4 fv[PPL];
+    float w0[PPL], w1[PPL];
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
         const int64_t p = lane + j * kWave;
-        a[j] = c[j] = 0.0f;
+        fv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        w0[j] = w1[j] = 0.0f;
         if (2 * p < d) {
-            a[j] = D::load(x[2 * p]);
-            c[j] = D::load(x[2 * p + 1]);
+            fv[j] = f[p];   // f[p][0][0], f[p][0][1], f[p][1][0], f[p][1][1]
+            w0[j] = D::load(w[2 * p]);
+            w1[j] = D::load(w[2 * p + 1]);
         }
-        sum += a[j] * a[j];
-        sum += c[j] * c[j];
     }
+    const float inv_d = 1.0f / static_cast<float>(d);
+    for (int64_t h0 = 0; h0 < heads; h0 += kHeadGroup) {
+        float a[kHeadGroup][PPL], c[kHeadGroup][PPL], sum[kHeadGroup];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
-    const float r = 1.0f / sqrtf(sum * (1.0f / static_cast<float>(d)) + eps);
+        for (int g = 0; g < kHeadGroup; ++g) {
+            sum[g] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < PPL; ++j) {
-        const int64_t p = lane + j * kWave;
-        if (2 * p >= d) break;
-        const float m0 = D::round(a[j] * r * D::load(w[2 * p]));
-        const float m1 = D::round(c[j] * r * D::load(w[2 * p + 1]));
-        const float4 fv = reinterpret_cast<const float4*>(f)[p];   // f[p][0][0], f[p][0][1], f[p][1][0], f[p][1][1]
-        o[2 * p] = D::store(fv.x * m0 + fv.y * m1);
-        o[2 * p + 1] = D::store(fv.z * m0 + fv.w * m1);
+            for (int j = 0; j < PPL; ++j) {
+                const int64_t p = lane + j * kWave;
+                a[g][j] = c[g][j] = 0.0f;
+                if (h0 + g < heads && 2 * p < d) load_pair<DT, PAIR>(x, (h0 + g) * d + 2 * p, a[g][j], c[g][j]);
+                sum[g] += a[g][j] * a[g][j];
+                sum[g] += c[g][j] * c[g][j];
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+            for (int g = 0; g < kHeadGroup; ++g) sum[g] += __shfl_xor(sum[g], off, kWave);
+        }
+#pragma unroll
+        for (int g = 0; g < kHeadGroup; ++g) {
+            if (h0 + g >= heads) break;
+            const float r = 1.0f / sqrtf(sum[g] * inv_d + eps);
+#pragma unroll
+            for (int j = 0; j < PPL; ++j) {
+                const int64_t p = lane + j * kWave;
+                if (2 * p >= d) break;
+                const float m0 = D::round(a[g][j] * r * w0[j]);
+                const float m1 = D::round(c[g][j] * r * w1[j]);
+                store_pair<DT, PAIR>(o, (h0 + g) * d + 2 * p, fv[j].x * m0 + fv[j].y * m1,
+                                     fv[j].z * m0 + fv[j].w * m1);
+            }
+        }
+    }
+}
+
+// The same operation for 16-bit rows of d = 8 * LPR (64, 128, 256), aligned
+// to 16 bytes: LPR lanes per row, each lane 8 consecutive elements (one
+// 16-byte load and store), 64 / LPR of the token's heads per wave
+// instruction, so a row costs log2(LPR) butterfly steps and one rsqrt over 8
+// elements per lane.  The lane's 4 rotation pairs and 8 weights sit in
+// registers for the whole token.  Same numerics per element as
+// rms_rope_tokens (the fp32 row sum adds in another order).
+template <int DT, int LPR>
+__global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restrict__ q, const void* __restrict__ k,
+                                                           const float* __restrict__ freqs,
+                                                           const void* __restrict__ q_scale,
+                                                           const void* __restrict__ k_scale,
+                                                           void* __restrict__ q_out, void* __restrict__ k_out,
+                                                           int64_t tokens, int64_t seq, int64_t heads,
+                                                           int64_t x_stride, int freq_per_batch, float eps) {
+    using D = DType<DT>;
+    using OS = typename D::storage;
+    static_assert(sizeof(OS) == 2, "16-bit rows only");
+    constexpr int d = 8 * LPR, kRows = kWave / LPR, kGroup = 3;
+    const int lane = threadIdx.x % kWave;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+    if (wave >= 2 * tokens) return;   // whole waves only; the kernel has no block barrier
+    const bool is_k = wave >= tokens;
+    const int64_t tok = is_k ? wave - tokens : wave;
+    const int sub = lane / LPR, col = lane % LPR;
+    const OS* x = static_cast<const OS*>(is_k ? k : q) + tok * x_stride + col * 8;
+    OS* o = static_cast<OS*>(is_k ? k_out : q_out) + tok * heads * d + col * 8;
+    const int64_t b = tok / seq, t = tok % seq;
+    const float4* f = reinterpret_cast<const float4*>(freqs + ((freq_per_batch ? b * seq : 0) + t) * (d / 2) * 4) +
+                      col * 4;
+    float4 fv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fv[i] = f[i];   // pair i: f[0][0], f[0][1], f[1][0], f[1][1]
+    float w[8];
+    {
+        const uint4 wv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(is_k ? k_scale : q_scale) + col * 8);
+        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[2 * i] = D::load(static_cast<uint16_t>(ww[i] & 0xffffu));
+            w[2 * i + 1] = D::load(static_cast<uint16_t>(ww[i] >> 16));
+        }
+    }
+    const float inv_d = 1.0f / static_cast<float>(d);
+    for (int64_t h0 = 0; h0 < heads; h0 += kRows * kGroup) {
+        float v[kGroup][8], sum[kGroup];
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g) {
+            const int64_t h = h0 + g * kRows + sub;
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (h < heads) u = *reinterpret_cast<const uint4*>(x + h * d);
+            const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+            sum[g] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[g][2 * i] = D::load(static_cast<uint16_t>(uu[i] & 0xffffu));
+                v[g][2 * i + 1] = D::load(static_cast<uint16_t>(uu[i] >> 16));
+                sum[g] += v[g][2 * i] * v[g][2 * i];
+                sum[g] += v[g][2 * i + 1] * v[g][2 * i + 1];
+            }
+        }
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) {
+#pragma unroll
+            for (int g = 0; g < kGroup; ++g) sum[g] += __shfl_xor(sum[g], off, kWave);
+        }
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g) {
+            const int64_t h = h0 + g * kRows + sub;
+            if (h >= heads) continue;
+            const float r = 1.0f / sqrtf(sum[g] * inv_d + eps);
+            uint32_t out[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float m0 = D::round(v[g][2 * i] * r * w[2 * i]);
+                const float m1 = D::round(v[g][2 * i + 1] * r * w[2 * i + 1]);
+                out[i] = D::store2(fv[i].x * m0 + fv[i].y * m1, fv[i].z * m0 + fv[i].w * m1);
+            }
+            *reinterpret_cast<uint4*>(o + h * d) = make_uint4(out[0], out[1], out[2], out[3]);
+        }
     }
 }
 
@@ -585,16 +730,35 @@ void launch_gated_residual(const void* x, const void* y, const void* gate0, cons
 
 bool launch_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
                      void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
-                     bool freq_per_batch, float eps, int dtype, hipStream_t stream) {
-    const int64_t rows = batch * seq * heads;
-    const dim3 grid(static_cast<unsigned>((2 * rows + 3) / 4)), block(256);
+                     int64_t x_stride, bool freq_per_batch, float eps, int dtype, hipStream_t stream) {
+    const int64_t tokens = batch * seq;
+    const dim3 grid(static_cast<unsigned>((2 * tokens + 3) / 4)), block(256);
     const int fpb = freq_per_batch ? 1 : 0;
-#define W8A8_RR(DT, PPL) hipLaunchKernelGGL((rms_rope_rows<DT, PPL>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, rows, seq, heads, d, fpb, eps)
     const int ppl = d <= 128 ? 1 : d <= 256 ? 2 : 0;
     if (ppl == 0) return false;
-    if (dtype == W8A8_BF16) { if (ppl == 1) W8A8_RR(W8A8_BF16, 1); else W8A8_RR(W8A8_BF16, 2); }
-    else if (dtype == W8A8_F16) { if (ppl == 1) W8A8_RR(W8A8_F16, 1); else W8A8_RR(W8A8_F16, 2); }
-    else { if (ppl == 1) W8A8_RR(W8A8_F32, 1); else W8A8_RR(W8A8_F32, 2); }
+    const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (dtype != W8A8_F32 && (d == 64 || d == 128 || d == 256) && x_stride % 8 == 0 && a16(q) && a16(k) &&
+        a16(q_out) && a16(k_out) && a16(q_scale) && a16(k_scale)) {
+#define W8A8_RV(DT, LPR) hipLaunchKernelGGL((rms_rope_tokens_vec<DT, LPR>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, x_stride, fpb, eps)
+#define W8A8_RV_D(DT) do { if (d == 64) W8A8_RV(DT, 8); else if (d == 128) W8A8_RV(DT, 16); else W8A8_RV(DT, 32); } while (0)
+        if (dtype == W8A8_BF16) W8A8_RV_D(W8A8_BF16);
+        else W8A8_RV_D(W8A8_F16);
+#undef W8A8_RV_D
+#undef W8A8_RV
+        return true;
+    }
+    const uintptr_t al = 2 * (dtype == W8A8_F32 ? 4 : 2);
+    const bool pair = x_stride % 2 == 0 && reinterpret_cast<uintptr_t>(q) % al == 0 &&
+                      reinterpret_cast<uintptr_t>(k) % al == 0 && reinterpret_cast<uintptr_t>(q_out) % al == 0 &&
+                      reinterpret_cast<uintptr_t>(k_out) % al == 0;
+#define W8A8_RR(DT, PPL, PAIR) hipLaunchKernelGGL((rms_rope_tokens<DT, PPL, PAIR>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, d, x_stride, fpb, eps)
+#define W8A8_RR_P(DT, PPL) do { if (pair) W8A8_RR(DT, PPL, true); else W8A8_RR(DT, PPL, false); } while (0)
+#define W8A8_RR_D(DT) do { if (ppl == 1) W8A8_RR_P(DT, 1); else W8A8_RR_P(DT, 2); } while (0)
+    if (dtype == W8A8_BF16) W8A8_RR_D(W8A8_BF16);
+    else if (dtype == W8A8_F16) W8A8_RR_D(W8A8_F16);
+    else W8A8_RR_D(W8A8_F32);
+#undef W8A8_RR_D
+#undef W8A8_RR_P
 #undef W8A8_RR
     return true;
 }

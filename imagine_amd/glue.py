@@ -205,7 +205,10 @@ def rms_rope(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6):
     eager_rms :204-222 / eager_apply :146-159, non-split): RMSNorm of every
     head row of q and k with its weight, then the pairwise rotation by
     ``freqs_cis``.  q, k [B, S, H, D]; freqs_cis fp32 [B|1, S, 1, D/2, 2, 2]
-    (the DiT's layout); scales [D].  Returns (q_out, k_out)."""
+    (the DiT's layout); scales [D].  q and k may be views whose heads are
+    packed but whose tokens are further apart (q, k = qkv[:, :, 0],
+    qkv[:, :, 1] of a [B, S, 3, H, D] QKV output): those are read in place.
+    Returns packed (q_out, k_out)."""
     _require_cuda(q, k, freqs_cis, q_scale)
     k_scale = q_scale if k_scale is None else k_scale
     if q.dim() != 4 or k.shape != q.shape:
@@ -218,11 +221,15 @@ def rms_rope(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6):
         raise NotImplementedError(f"rms_rope: freqs_cis layout {fs} is not part of this build")
     if any(t.dtype != q.dtype for t in (k, q_scale, k_scale)):
         raise RuntimeError("rms_rope: k and the scales must have the dtype of q")
-    q, k = q.contiguous(), k.contiguous()
+    rs = q.stride(1)
+    if q.stride() != (s * rs, rs, d, 1) or k.stride() != q.stride() or rs < h * d:
+        q, k = q.contiguous(), k.contiguous()
+        rs = h * d
     f = freqs_cis.contiguous()
     qs, ks = q_scale.reshape(-1).contiguous(), k_scale.reshape(-1).contiguous()
-    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    qo = torch.empty((b, s, h, d), device=q.device, dtype=q.dtype)
+    ko = torch.empty_like(qo)
     _lib.check(_lib.load().w8a8_rms_rope(
-        _ptr(q), _ptr(k), _ptr(f), _ptr(qs), _ptr(ks), _ptr(qo), _ptr(ko), b, s, h, d, 1 if fs[0] == b and b > 1 else 0,
+        _ptr(q), _ptr(k), _ptr(f), _ptr(qs), _ptr(ks), _ptr(qo), _ptr(ko), b, s, h, d, rs, 1 if fs[0] == b and b > 1 else 0,
         float(epsilon), _dtype_code(q.dtype, "rms_rope"), _stream(q.device)))
     return qo, ko

@@ -263,15 +263,18 @@ int w8a8_modulated_norm_quant(const void* x, const void* scale0, const void* sca
 /* QK RMSNorm + RoPE of the DiT attention: Kitchen's "rms_rope" call
  * (inference/src/backend_rope.rs:311-345) with the numerics of the crate's
  * eager route (eager_rms :204-222, eager_apply :146-159, non-split, whole
- * head rotated).  q, k, q_out, k_out [batch, seq, heads, d] in dtype; q_scale,
- * k_scale [d] in dtype; freqs fp32 [freq_per_batch ? batch : 1, seq, d/2, 2, 2]
- * (the reference's [B|1, S, 1, d/2, 2, 2]), 16-byte aligned.  Per row:
- *   m = T(T(x * rsqrt(mean(x^2) + eps)) * scale)
+ * head rotated).  q, k [batch, seq, heads, d] in dtype with the heads of a
+ * token packed d apart and consecutive tokens x_row_stride elements apart
+ * (heads * d when packed; 3 * heads * d for views into a fused QKV output);
+ * q_out, k_out packed [batch, seq, heads, d]; q_scale, k_scale [d] in dtype;
+ * freqs fp32 [freq_per_batch ? batch : 1, seq, d/2, 2, 2] (the reference's
+ * [B|1, S, 1, d/2, 2, 2]), 16-byte aligned.  Per row:
+ *   m = T(x * rsqrt(mean(x^2) + eps) * scale)   (aten rms_norm: fp32, one rounding)
  *   out[2i + j] = T(f[i][j][0] * m[2i] + f[i][j][1] * m[2i + 1])   (fp32)
- * d even, at most 256. */
+ * d even, at most 256; x_row_stride >= heads * d. */
 int w8a8_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
-                  void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d, int freq_per_batch,
-                  double eps, int dtype, hipStream_t stream);
+                  void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
+                  int64_t x_row_stride, int freq_per_batch, double eps, int dtype, hipStream_t stream);
 
 /* Gated residual of the DiT block (inference/src/models/qwen_image21/
  * numeric.rs:110-125): x, y [batch, tokens, d], gates [batch, d];

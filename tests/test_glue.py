@@ -182,9 +182,11 @@ def test_rms_rope_host_errors():
     with pytest.raises(RuntimeError):
         W.rms_rope(q, q, torch.zeros(1, 4, 1, 4, 2, 2), torch.ones(8, dtype=torch.bfloat16))   # CPU tensors
     lib = _lib.load()
-    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 1, 4, 2, 7, 0, 1e-6, _lib.BF16,
+    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 1, 4, 2, 7, 14, 0, 1e-6, _lib.BF16,
                              None) == _lib.ERR_VALUE
-    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 0, 4, 2, 8, 0, 1e-6, _lib.BF16,
+    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 0, 4, 2, 8, 16, 0, 1e-6, _lib.BF16,
                              None) == _lib.OK
-    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 1, 4, 2, 8, 0, 1e-6, _lib.BF16,
-                             None) == _lib.ERR_VALUE
+    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 1, 4, 2, 8, 16, 0, 1e-6, _lib.BF16,
+                             None) == _lib.ERR_VALUE                  # null pointers
+    assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 1, 4, 2, 8, 15, 0, 1e-6, _lib.BF16,
+                             None) == _lib.ERR_VALUE                  # token rows overlap

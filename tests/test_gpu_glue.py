@@ -204,19 +204,34 @@ def _freqs(batch, seq, d, seed):
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("fb", [1, 2])
-def test_rms_rope_matches_eager_sequence(dtype, fb):
+@pytest.mark.parametrize("layout", ["packed", "qkv_view"])
+@pytest.mark.parametrize("D", [128, 64, 256, 96])
+def test_rms_rope_matches_eager_sequence(dtype, fb, layout, D):
     """QK RMSNorm + RoPE against the reference's eager sequence (rms_norm with
     weight, then the fp32 pair rotation) on the CPU: two ulps of the rotated
     pair's magnitude, and at least 97% of outputs bit-equal (the fp32 sum of
-    squares rounds in another order)."""
+    squares rounds in another order).  q and k either packed or read in place
+    as views into one [B, S, 3, H, D] QKV output; the 16-byte-per-lane rows
+    (D = 64, 128, 256) and the pair-per-lane kernel (D = 96)."""
+    if D != 128 and (layout != "packed" or fb != 1):
+        pytest.skip("other head dims run once, packed")
     g = torch.Generator().manual_seed(52 + fb)
-    B, S, H, D = 2, 300, 24, 128
-    q = (torch.randn(B, S, H, D, generator=g) * 2).to(TD[dtype])
-    k = (torch.randn(B, S, H, D, generator=g) * 0.5).to(TD[dtype])
+    B, S, H = 2, 300, 24 if D == 128 else 5
+    if layout == "packed":
+        q = (torch.randn(B, S, H, D, generator=g) * 2).to(TD[dtype])
+        k = (torch.randn(B, S, H, D, generator=g) * 0.5).to(TD[dtype])
+        qd, kd = q.to(DEV), k.to(DEV)
+    else:
+        qkv = (torch.randn(B, S, 3, H, D, generator=g) * torch.tensor([2.0, 0.5, 1.0])[:, None, None]).to(TD[dtype])
+        q, k = qkv[:, :, 0].contiguous(), qkv[:, :, 1].contiguous()
+        qkv_d = qkv.to(DEV)
+        qd, kd = qkv_d[:, :, 0], qkv_d[:, :, 1]
+        assert qd.stride(1) == 3 * H * D
     qs = (1 + 0.1 * torch.randn(D, generator=g)).to(TD[dtype])
     ks = (1 + 0.1 * torch.randn(D, generator=g)).to(TD[dtype])
     f = _freqs(fb, S, D, seed=53)
-    qo, ko = W.rms_rope(q.to(DEV), k.to(DEV), f.to(DEV), qs.to(DEV), ks.to(DEV), 1e-6)
+    qo, ko = W.rms_rope(qd, kd, f.to(DEV), qs.to(DEV), ks.to(DEV), 1e-6)
+    assert qo.is_contiguous() and ko.is_contiguous()
     wq, wk = E.rms_rope(q, k, f, qs, ks, 1e-6)
     for got, want, x, s in ((qo, wq, q, qs), (ko, wk, k, ks)):
         m = torch.nn.functional.rms_norm(x, (D,), s, 1e-6).float()
