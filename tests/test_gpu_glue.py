@@ -237,3 +237,35 @@ def test_rms_rope_matches_eager_sequence(dtype, fb, layout, D):
         m = torch.nn.functional.rms_norm(x, (D,), s, 1e-6).float()
         mag = (m[..., 0::2].abs() + m[..., 1::2].abs()).repeat_interleave(2, -1).numpy()
         close(storage(got, dtype), storage(want, dtype), dtype, before_add=mag)
+
+
+@pytest.mark.parametrize("case", ["f32", "bf16_unaligned"])
+def test_rms_rope_pair_kernel_fp32_and_unaligned(case):
+    """The pair-per-lane kernel on fp32 rows (nothing is rounded between the
+    steps, so outputs agree up to the fp32 row-sum order: no bit-equal share
+    asked) and on bf16 q / k that start 2 bytes off a 4-byte boundary
+    (element-wise loads and stores)."""
+    dtype = "f32" if case == "f32" else "bf16"
+    g = torch.Generator().manual_seed(61)
+    B, S, H, D = 2, 200, 6, 128
+    q = (torch.randn(B, S, H, D, generator=g) * 2).to(TD[dtype])
+    k = (torch.randn(B, S, H, D, generator=g) * 0.5).to(TD[dtype])
+
+    def offset_by_one(t):
+        buf = torch.zeros(t.numel() + 1, dtype=t.dtype, device=DEV)
+        buf[1:] = t.reshape(-1).to(DEV)
+        v = buf[1:].view(t.shape)
+        assert v.data_ptr() % 4 == 2
+        return v
+
+    qd, kd = (q.to(DEV), k.to(DEV)) if case == "f32" else (offset_by_one(q), offset_by_one(k))
+    qs = (1 + 0.1 * torch.randn(D, generator=g)).to(TD[dtype])
+    ks = (1 + 0.1 * torch.randn(D, generator=g)).to(TD[dtype])
+    f = _freqs(1, S, D, seed=62)
+    qo, ko = W.rms_rope(qd, kd, f.to(DEV), qs.to(DEV), ks.to(DEV), 1e-6)
+    wq, wk = E.rms_rope(q, k, f, qs, ks, 1e-6)
+    for got, want, x, s in ((qo, wq, q, qs), (ko, wk, k, ks)):
+        m = torch.nn.functional.rms_norm(x, (D,), s, 1e-6).float()
+        mag = (m[..., 0::2].abs() + m[..., 1::2].abs()).repeat_interleave(2, -1).numpy()
+        close(storage(got, dtype), storage(want, dtype), dtype, frac=0.0 if dtype == "f32" else 0.97,
+              before_add=mag)
