@@ -14,9 +14,9 @@ Also measured and reported beside it: per-linear TOPS, the per-token
 quantizer's GB/s (M=11712, K=3072 and K=12288), the adaLN GEMV's GB/s
 (M=2, K=3072, N=18432), and fused vs unfused quant+GEMM on the outlier
 workload (M=11712, K=3072, N=12288, Student-t(3) activations), the block
-glue's GB/s (adaLN, gated residual at 2x5856x3072), and the 60-block DiT
-denoising step at M=19904 (ms/step, W8A8 and glue shares; attention, QK
-RMSNorm and RoPE in torch).  The memory-bound kernels rotate through enough
+glue's GB/s (adaLN, gated residual at 2x5856x3072; QK RMSNorm + RoPE on q / k
+views into a 2x5856x3x24x128 QKV output), and the 60-block DiT denoising step
+at M=19904 (ms/step, W8A8 and glue shares; attention in torch).  The memory-bound kernels rotate through enough
 buffer sets to exceed the 256 MB Infinity Cache so they measure HBM, not cache.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--only KERNEL] [--no-cpu] [--no-dit-step]
@@ -45,7 +45,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--only", default=None,
                    help="run only one kernel in a loop (for rocprofv3 counters): "
-                        "up_gemm | quant | convrot_quant | step | copy | dit_step")
+                        "up_gemm | quant | convrot_quant | rms_rope | step | copy | dit_step")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-dit-step", action="store_true", help="skip the 60-block DiT step extra")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -525,6 +525,18 @@ def run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs):
     elif args.only == "step":
         for _ in range(n_iter):
             step()
+    elif args.only == "rms_rope":
+        # QK RMSNorm + RoPE on q / k views into a [2, 5856, 3, 24, 128] bf16 QKV output
+        hb, ht, nh, hd = 2, M_TOK // 2, 24, HID // 24
+        qkv = torch.randn(hb, ht, 3, nh, hd, device=dev).to(torch.bfloat16)
+        qo = torch.empty(hb, ht, nh, hd, device=dev, dtype=torch.bfloat16)
+        ko = torch.empty_like(qo)
+        fr = torch.randn(ht, hd // 2, 2, 2, device=dev)
+        sc = torch.ones(hd, device=dev, dtype=torch.bfloat16)
+        for _ in range(n_iter):
+            W._lib.check(lib.w8a8_rms_rope(qkv.data_ptr(), qkv[:, :, 1].data_ptr(), fr.data_ptr(), sc.data_ptr(),
+                                           sc.data_ptr(), qo.data_ptr(), ko.data_ptr(), hb, ht, nh, hd, 3 * nh * hd,
+                                           0, 1e-6, W._lib.BF16, torch.cuda.current_stream().cuda_stream))
     elif args.only == "copy":
         # counter calibration: a plain device copy of known size (1 GiB read,
         # 1 GiB written per launch) for scaling FETCH_SIZE / WRITE_SIZE
