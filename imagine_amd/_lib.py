@@ -50,6 +50,7 @@ SIGNATURES = {
     "w8a8_adaln": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, ctypes.c_double, _i, _i, _p]),
     "w8a8_gated_residual": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i, _p]),
     "w8a8_rms_rope": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, ctypes.c_double, _i, _p]),
+    "w8a8_apply_rope": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, _i, _p]),
     "w8a8_modulated_norm_quant": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, ctypes.c_double, _i,
                                        _i, _u32, _p]),
     "w8a8_quantize_rowwise_modulated": (_i, [_p, _i, _p, _p, _p, _i64, _i64, _u32, _p]),

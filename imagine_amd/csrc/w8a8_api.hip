@@ -44,7 +44,8 @@ void launch_quant_modulated(const void* x, int dtype, const void* mod, int8_t* q
                             int64_t K, int recip, hipStream_t stream);
 bool launch_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
                      void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
-                     int64_t x_stride, bool freq_per_batch, float eps, int dtype, hipStream_t stream);
+                     int64_t x_stride, bool freq_per_batch, float eps, bool norm, int dtype,
+                     hipStream_t stream);
 bool launch_modnorm_quant(const void* x, const void* s0, const void* s1, const void* h0, const void* h1, int8_t* q,
                           float* xs, int64_t rows, int64_t tokens, int64_t d, int64_t prefix, float eps, int dtype,
                           bool rms, int recip, hipStream_t stream);
@@ -103,6 +104,32 @@ int check_residual(const void* rscale, int64_t rscale_size, const void* resid, i
     if (rscale_size != 1 && rscale_size != N)
         return fail(W8A8_ERR_RUNTIME, "residual_scale must be scalar or per-output-channel");
     return W8A8_OK;
+}
+
+}  // namespace
+
+namespace {
+
+// Shared checks and launch of the RoPE family (norm: rms_rope / rms_rope1;
+// otherwise apply_rope / apply_rope1; k == nullptr: the one-tensor forms).
+int rope_entry(const char* name, const void* q, const void* k, const float* freqs, const void* q_scale,
+               const void* k_scale, void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
+               int64_t x_row_stride, int freq_per_batch, double eps, bool norm, int dtype, hipStream_t stream) {
+    const std::string n(name);
+    if (batch < 0 || seq < 0 || heads < 0 || d < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (!valid_dtype(dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported dtype for " + n);
+    if (d % 2 != 0 || d > 256) return fail(W8A8_ERR_VALUE, n + " needs an even head dimension of at most 256");
+    if (batch == 0 || seq == 0 || heads == 0 || d == 0) return W8A8_OK;
+    if (x_row_stride < heads * d) return fail(W8A8_ERR_VALUE, n + ": x_row_stride must be at least heads * d");
+    if (!q || !freqs || !q_out || (norm && !q_scale)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (k && (!k_out || (norm && !k_scale))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (reinterpret_cast<uintptr_t>(freqs) % 16 != 0) return fail(W8A8_ERR_VALUE, "freqs must be 16-byte aligned");
+    if (2 * batch * seq > 0x7fffffffll * 4) return fail(W8A8_ERR_VALUE, n + ": too many tokens");
+    if (!w8a8::launch_rms_rope(q, k, freqs, q_scale, k ? k_scale : nullptr, q_out, k ? k_out : nullptr, batch, seq,
+                               heads, d, x_row_stride, freq_per_batch != 0, static_cast<float>(eps), norm, dtype,
+                               stream))
+        return fail(W8A8_ERR_VALUE, n + " needs an even head dimension of at most 256");
+    return check_launch(name);
 }
 
 }  // namespace
@@ -175,19 +202,15 @@ int w8a8_modulated_norm_quant(const void* x, const void* scale0, const void* sca
 int w8a8_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
                   void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
                   int64_t x_row_stride, int freq_per_batch, double eps, int dtype, hipStream_t stream) {
-    if (batch < 0 || seq < 0 || heads < 0 || d < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
-    if (!valid_dtype(dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported dtype for rms_rope");
-    if (d % 2 != 0 || d > 256) return fail(W8A8_ERR_VALUE, "rms_rope needs an even head dimension of at most 256");
-    if (batch == 0 || seq == 0 || heads == 0 || d == 0) return W8A8_OK;
-    if (x_row_stride < heads * d) return fail(W8A8_ERR_VALUE, "rms_rope: x_row_stride must be at least heads * d");
-    if (!q || !k || !freqs || !q_scale || !k_scale || !q_out || !k_out) return fail(W8A8_ERR_VALUE, "null tensor pointer");
-    if (reinterpret_cast<uintptr_t>(freqs) % 16 != 0) return fail(W8A8_ERR_VALUE, "freqs must be 16-byte aligned");
-    if (2 * batch * seq > 0x7fffffffll * 4) return fail(W8A8_ERR_VALUE, "rms_rope: too many tokens");
-    if (!w8a8::launch_rms_rope(q, k, freqs, q_scale, k_scale, q_out, k_out, batch, seq, heads, d, x_row_stride,
-                               freq_per_batch != 0,
-                               static_cast<float>(eps), dtype, stream))
-        return fail(W8A8_ERR_VALUE, "rms_rope needs an even head dimension of at most 256");
-    return check_launch("rms_rope");
+    return rope_entry("rms_rope", q, k, freqs, q_scale, k_scale, q_out, k_out, batch, seq, heads, d, x_row_stride,
+                      freq_per_batch, eps, true, dtype, stream);
+}
+
+int w8a8_apply_rope(const void* x, const void* k, const float* freqs, void* out, void* k_out, int64_t batch,
+                    int64_t seq, int64_t heads, int64_t d, int64_t x_row_stride, int freq_per_batch, int dtype,
+                    hipStream_t stream) {
+    return rope_entry("apply_rope", x, k, freqs, nullptr, nullptr, out, k_out, batch, seq, heads, d, x_row_stride,
+                      freq_per_batch, 0.0, false, dtype, stream);
 }
 
 int w8a8_gated_residual(const void* x, const void* y, const void* gate0, const void* gate1, void* out,

@@ -312,6 +312,9 @@ __global__ __launch_bounds__(NT) void modnorm_quant_rows_vec(
 // q / k read straight out of a fused QKV output), its heads d apart; the
 // outputs are packed [batch, seq, heads, d].  PAIR: every pair is read and
 // written as one 2-element access (row bases aligned to two elements).
+// NORM = false is the rotation alone (Kitchen's apply_rope / apply_rope1, the
+// eager route backend_rope.rs:146-159): m = x, exact in fp32.  k == nullptr
+// (ntensors = 1) is the one-tensor form (rms_rope1 / apply_rope1).
 constexpr int kHeadGroup = 8;
 
 template <int DT, bool PAIR>
@@ -345,19 +348,19 @@ __device__ __forceinline__ void store_pair(typename DType<DT>::storage* o, int64
     }
 }
 
-template <int DT, int PPL, bool PAIR>
+template <int DT, int PPL, bool PAIR, bool NORM>
 __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ q, const void* __restrict__ k,
                                                        const float* __restrict__ freqs,
                                                        const void* __restrict__ q_scale,
                                                        const void* __restrict__ k_scale, void* __restrict__ q_out,
                                                        void* __restrict__ k_out, int64_t tokens, int64_t seq,
                                                        int64_t heads, int64_t d, int64_t x_stride,
-                                                       int freq_per_batch, float eps) {
+                                                       int ntensors, int freq_per_batch, float eps) {
     using D = DType<DT>;
     using OS = typename D::storage;
     const int lane = threadIdx.x % kWave;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
-    if (wave >= 2 * tokens) return;   // whole waves only; the kernel has no block barrier
+    if (wave >= ntensors * tokens) return;   // whole waves only; the kernel has no block barrier
     const bool is_k = wave >= tokens;
     const int64_t tok = is_k ? wave - tokens : wave;
     const OS* x = static_cast<const OS*>(is_k ? k : q) + tok * x_stride;
@@ -374,8 +377,10 @@ __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ 
         w0[j] = w1[j] = 0.0f;
         if (2 * p < d) {
             fv[j] = f[p];   // f[p][0][0], f[p][0][1], f[p][1][0], f[p][1][1]
-            w0[j] = D::load(w[2 * p]);
-            w1[j] = D::load(w[2 * p + 1]);
+            if constexpr (NORM) {
+                w0[j] = D::load(w[2 * p]);
+                w1[j] = D::load(w[2 * p + 1]);
+            }
         }
     }
     const float inv_d = 1.0f / static_cast<float>(d);
@@ -393,21 +398,23 @@ __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ 
                 sum[g] += c[g][j] * c[g][j];
             }
         }
+        if constexpr (NORM) {
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
+            for (int off = 32; off > 0; off >>= 1) {
 #pragma unroll
-            for (int g = 0; g < kHeadGroup; ++g) sum[g] += __shfl_xor(sum[g], off, kWave);
+                for (int g = 0; g < kHeadGroup; ++g) sum[g] += __shfl_xor(sum[g], off, kWave);
+            }
         }
 #pragma unroll
         for (int g = 0; g < kHeadGroup; ++g) {
             if (h0 + g >= heads) break;
-            const float r = 1.0f / sqrtf(sum[g] * inv_d + eps);
+            const float r = NORM ? 1.0f / sqrtf(sum[g] * inv_d + eps) : 1.0f;
 #pragma unroll
             for (int j = 0; j < PPL; ++j) {
                 const int64_t p = lane + j * kWave;
                 if (2 * p >= d) break;
-                const float m0 = D::round(a[g][j] * r * w0[j]);
-                const float m1 = D::round(c[g][j] * r * w1[j]);
+                const float m0 = NORM ? D::round(a[g][j] * r * w0[j]) : a[g][j];
+                const float m1 = NORM ? D::round(c[g][j] * r * w1[j]) : c[g][j];
                 store_pair<DT, PAIR>(o, (h0 + g) * d + 2 * p, fv[j].x * m0 + fv[j].y * m1,
                                      fv[j].z * m0 + fv[j].w * m1);
             }
@@ -422,21 +429,22 @@ __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ 
 // elements per lane.  The lane's 4 rotation pairs and 8 weights sit in
 // registers for the whole token.  Same numerics per element as
 // rms_rope_tokens (the fp32 row sum adds in another order).
-template <int DT, int LPR>
+template <int DT, int LPR, bool NORM>
 __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restrict__ q, const void* __restrict__ k,
                                                            const float* __restrict__ freqs,
                                                            const void* __restrict__ q_scale,
                                                            const void* __restrict__ k_scale,
                                                            void* __restrict__ q_out, void* __restrict__ k_out,
                                                            int64_t tokens, int64_t seq, int64_t heads,
-                                                           int64_t x_stride, int freq_per_batch, float eps) {
+                                                           int64_t x_stride, int ntensors, int freq_per_batch,
+                                                           float eps) {
     using D = DType<DT>;
     using OS = typename D::storage;
     static_assert(sizeof(OS) == 2, "16-bit rows only");
     constexpr int d = 8 * LPR, kRows = kWave / LPR, kGroup = 3;
     const int lane = threadIdx.x % kWave;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
-    if (wave >= 2 * tokens) return;   // whole waves only; the kernel has no block barrier
+    if (wave >= ntensors * tokens) return;   // whole waves only; the kernel has no block barrier
     const bool is_k = wave >= tokens;
     const int64_t tok = is_k ? wave - tokens : wave;
     const int sub = lane / LPR, col = lane % LPR;
@@ -448,8 +456,8 @@ __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restric
     float4 fv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) fv[i] = f[i];   // pair i: f[0][0], f[0][1], f[1][0], f[1][1]
-    float w[8];
-    {
+    float w[8] = {};
+    if constexpr (NORM) {
         const uint4 wv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(is_k ? k_scale : q_scale) + col * 8);
         const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
@@ -476,21 +484,23 @@ __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restric
                 sum[g] += v[g][2 * i + 1] * v[g][2 * i + 1];
             }
         }
+        if constexpr (NORM) {
 #pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1) {
+            for (int off = LPR / 2; off > 0; off >>= 1) {
 #pragma unroll
-            for (int g = 0; g < kGroup; ++g) sum[g] += __shfl_xor(sum[g], off, kWave);
+                for (int g = 0; g < kGroup; ++g) sum[g] += __shfl_xor(sum[g], off, kWave);
+            }
         }
 #pragma unroll
         for (int g = 0; g < kGroup; ++g) {
             const int64_t h = h0 + g * kRows + sub;
             if (h >= heads) continue;
-            const float r = 1.0f / sqrtf(sum[g] * inv_d + eps);
+            const float r = NORM ? 1.0f / sqrtf(sum[g] * inv_d + eps) : 1.0f;
             uint32_t out[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float m0 = D::round(v[g][2 * i] * r * w[2 * i]);
-                const float m1 = D::round(v[g][2 * i + 1] * r * w[2 * i + 1]);
+                const float m0 = NORM ? D::round(v[g][2 * i] * r * w[2 * i]) : v[g][2 * i];
+                const float m1 = NORM ? D::round(v[g][2 * i + 1] * r * w[2 * i + 1]) : v[g][2 * i + 1];
                 out[i] = D::store2(fv[i].x * m0 + fv[i].y * m1, fv[i].z * m0 + fv[i].w * m1);
             }
             *reinterpret_cast<uint4*>(o + h * d) = make_uint4(out[0], out[1], out[2], out[3]);
@@ -730,28 +740,33 @@ void launch_gated_residual(const void* x, const void* y, const void* gate0, cons
 
 bool launch_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
                      void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
-                     int64_t x_stride, bool freq_per_batch, float eps, int dtype, hipStream_t stream) {
+                     int64_t x_stride, bool freq_per_batch, float eps, bool norm, int dtype,
+                     hipStream_t stream) {
     const int64_t tokens = batch * seq;
-    const dim3 grid(static_cast<unsigned>((2 * tokens + 3) / 4)), block(256);
+    const int nt = k ? 2 : 1;
+    const dim3 grid(static_cast<unsigned>((nt * tokens + 3) / 4)), block(256);
     const int fpb = freq_per_batch ? 1 : 0;
     const int ppl = d <= 128 ? 1 : d <= 256 ? 2 : 0;
     if (ppl == 0) return false;
     const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (dtype != W8A8_F32 && (d == 64 || d == 128 || d == 256) && x_stride % 8 == 0 && a16(q) && a16(k) &&
         a16(q_out) && a16(k_out) && a16(q_scale) && a16(k_scale)) {
-#define W8A8_RV(DT, LPR) hipLaunchKernelGGL((rms_rope_tokens_vec<DT, LPR>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, x_stride, fpb, eps)
+#define W8A8_RV_N(DT, LPR, N) hipLaunchKernelGGL((rms_rope_tokens_vec<DT, LPR, N>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, x_stride, nt, fpb, eps)
+#define W8A8_RV(DT, LPR) do { if (norm) W8A8_RV_N(DT, LPR, true); else W8A8_RV_N(DT, LPR, false); } while (0)
 #define W8A8_RV_D(DT) do { if (d == 64) W8A8_RV(DT, 8); else if (d == 128) W8A8_RV(DT, 16); else W8A8_RV(DT, 32); } while (0)
         if (dtype == W8A8_BF16) W8A8_RV_D(W8A8_BF16);
         else W8A8_RV_D(W8A8_F16);
 #undef W8A8_RV_D
 #undef W8A8_RV
+#undef W8A8_RV_N
         return true;
     }
     const uintptr_t al = 2 * (dtype == W8A8_F32 ? 4 : 2);
     const bool pair = x_stride % 2 == 0 && reinterpret_cast<uintptr_t>(q) % al == 0 &&
                       reinterpret_cast<uintptr_t>(k) % al == 0 && reinterpret_cast<uintptr_t>(q_out) % al == 0 &&
                       reinterpret_cast<uintptr_t>(k_out) % al == 0;
-#define W8A8_RR(DT, PPL, PAIR) hipLaunchKernelGGL((rms_rope_tokens<DT, PPL, PAIR>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, d, x_stride, fpb, eps)
+#define W8A8_RR_N(DT, PPL, PAIR, N) hipLaunchKernelGGL((rms_rope_tokens<DT, PPL, PAIR, N>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, d, x_stride, nt, fpb, eps)
+#define W8A8_RR(DT, PPL, PAIR) do { if (norm) W8A8_RR_N(DT, PPL, PAIR, true); else W8A8_RR_N(DT, PPL, PAIR, false); } while (0)
 #define W8A8_RR_P(DT, PPL) do { if (pair) W8A8_RR(DT, PPL, true); else W8A8_RR(DT, PPL, false); } while (0)
 #define W8A8_RR_D(DT) do { if (ppl == 1) W8A8_RR_P(DT, 1); else W8A8_RR_P(DT, 2); } while (0)
     if (dtype == W8A8_BF16) W8A8_RR_D(W8A8_BF16);
@@ -760,6 +775,7 @@ bool launch_rms_rope(const void* q, const void* k, const float* freqs, const voi
 #undef W8A8_RR_D
 #undef W8A8_RR_P
 #undef W8A8_RR
+#undef W8A8_RR_N
     return true;
 }
 

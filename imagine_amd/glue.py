@@ -200,6 +200,42 @@ def modulated_norm_quant(x, scale, prefix, shift, eps, rms=False, *, scale_form=
     return q, s
 
 
+def _rope(name, q, k, freqs_cis, q_scale, k_scale, epsilon, norm):
+    """Checks, layout and launch shared by the non-split RoPE family; k None
+    is the one-tensor form.  Returns packed (q_out, k_out or None)."""
+    _require_cuda(*[t for t in (q, k, freqs_cis, q_scale) if t is not None])
+    if q.dim() != 4 or (k is not None and k.shape != q.shape):
+        raise RuntimeError(f"{name}: inputs must be [batch, seq, heads, head_dim] of one shape")
+    b, s, h, d = q.shape
+    if freqs_cis.dtype != torch.float32:
+        raise NotImplementedError(f"{name}: freqs_cis in a dtype other than float32 is not part of this build")
+    fs = tuple(freqs_cis.shape)
+    if len(fs) != 6 or fs[0] not in (1, b) or fs[1] != s or fs[2] != 1 or fs[3:] != (d // 2, 2, 2):
+        raise NotImplementedError(f"{name}: freqs_cis layout {fs} is not part of this build")
+    if any(t is not None and t.dtype != q.dtype for t in (k, q_scale, k_scale)):
+        raise RuntimeError(f"{name}: the second tensor and the scales must have the dtype of the first")
+    rs = q.stride(1)
+    if q.stride() != (s * rs, rs, d, 1) or (k is not None and k.stride() != q.stride()) or rs < h * d:
+        q = q.contiguous()
+        k = None if k is None else k.contiguous()
+        rs = h * d
+    f = freqs_cis.contiguous()
+    qo = torch.empty((b, s, h, d), device=q.device, dtype=q.dtype)
+    ko = None if k is None else torch.empty_like(qo)
+    fpb = 1 if fs[0] == b and b > 1 else 0
+    code = _dtype_code(q.dtype, name)
+    if norm:
+        qs = q_scale.reshape(-1).contiguous()
+        ks = None if k is None else k_scale.reshape(-1).contiguous()
+        _lib.check(_lib.load().w8a8_rms_rope(
+            _ptr(q), _ptr(k), _ptr(f), _ptr(qs), _ptr(ks), _ptr(qo), _ptr(ko), b, s, h, d, rs, fpb,
+            float(epsilon), code, _stream(q.device)))
+    else:
+        _lib.check(_lib.load().w8a8_apply_rope(
+            _ptr(q), _ptr(k), _ptr(f), _ptr(qo), _ptr(ko), b, s, h, d, rs, fpb, code, _stream(q.device)))
+    return qo, ko
+
+
 def rms_rope(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6):
     """Kitchen's ``rms_rope`` (backend_rope.rs:364-440, the eager numerics of
     eager_rms :204-222 / eager_apply :146-159, non-split): RMSNorm of every
@@ -209,27 +245,26 @@ def rms_rope(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6):
     packed but whose tokens are further apart (q, k = qkv[:, :, 0],
     qkv[:, :, 1] of a [B, S, 3, H, D] QKV output): those are read in place.
     Returns packed (q_out, k_out)."""
-    _require_cuda(q, k, freqs_cis, q_scale)
-    k_scale = q_scale if k_scale is None else k_scale
-    if q.dim() != 4 or k.shape != q.shape:
-        raise RuntimeError("rms_rope: q and k must be [batch, seq, heads, head_dim] of one shape")
-    b, s, h, d = q.shape
-    if freqs_cis.dtype != torch.float32:
-        raise NotImplementedError("rms_rope: freqs_cis in a dtype other than float32 is not part of this build")
-    fs = tuple(freqs_cis.shape)
-    if len(fs) != 6 or fs[0] not in (1, b) or fs[1] != s or fs[2] != 1 or fs[3:] != (d // 2, 2, 2):
-        raise NotImplementedError(f"rms_rope: freqs_cis layout {fs} is not part of this build")
-    if any(t.dtype != q.dtype for t in (k, q_scale, k_scale)):
-        raise RuntimeError("rms_rope: k and the scales must have the dtype of q")
-    rs = q.stride(1)
-    if q.stride() != (s * rs, rs, d, 1) or k.stride() != q.stride() or rs < h * d:
-        q, k = q.contiguous(), k.contiguous()
-        rs = h * d
-    f = freqs_cis.contiguous()
-    qs, ks = q_scale.reshape(-1).contiguous(), k_scale.reshape(-1).contiguous()
-    qo = torch.empty((b, s, h, d), device=q.device, dtype=q.dtype)
-    ko = torch.empty_like(qo)
-    _lib.check(_lib.load().w8a8_rms_rope(
-        _ptr(q), _ptr(k), _ptr(f), _ptr(qs), _ptr(ks), _ptr(qo), _ptr(ko), b, s, h, d, rs, 1 if fs[0] == b and b > 1 else 0,
-        float(epsilon), _dtype_code(q.dtype, "rms_rope"), _stream(q.device)))
-    return qo, ko
+    return _rope("rms_rope", q, k, freqs_cis, q_scale, q_scale if k_scale is None else k_scale, epsilon, True)
+
+
+def rms_rope1(x, freqs_cis, scale, epsilon=1e-6):
+    """Kitchen's ``rms_rope1`` (one tensor; backend_rope.rs:364-440): as
+    ``rms_rope`` on x alone.  Returns the packed output."""
+    return _rope("rms_rope1", x, None, freqs_cis, scale, None, epsilon, True)[0]
+
+
+def apply_rope(xq, xk, freqs_cis):
+    """Kitchen's ``apply_rope`` (backend_rope.rs:256-299, eager numerics
+    eager_apply :146-159, non-split): the pairwise rotation alone of xq and xk
+    [B, S, H, D] by fp32 ``freqs_cis`` [B|1, S, 1, D/2, 2, 2].  Returns packed
+    (xq_out, xk_out)."""
+    if xk is None:
+        raise RuntimeError("apply_rope: xk is required (apply_rope1 takes one tensor)")
+    return _rope("apply_rope", xq, xk, freqs_cis, None, None, 0.0, False)
+
+
+def apply_rope1(x, freqs_cis):
+    """Kitchen's ``apply_rope1`` (the DiT's attention-patch route,
+    models/qwen_image21/dit.rs:460-480): ``apply_rope`` on one tensor."""
+    return _rope("apply_rope1", x, None, freqs_cis, None, None, 0.0, False)[0]

@@ -271,10 +271,21 @@ int w8a8_modulated_norm_quant(const void* x, const void* scale0, const void* sca
  * [B|1, S, 1, d/2, 2, 2]), 16-byte aligned.  Per row:
  *   m = T(x * rsqrt(mean(x^2) + eps) * scale)   (aten rms_norm: fp32, one rounding)
  *   out[2i + j] = T(f[i][j][0] * m[2i] + f[i][j][1] * m[2i + 1])   (fp32)
- * d even, at most 256; x_row_stride >= heads * d. */
+ * d even, at most 256; x_row_stride >= heads * d.  k == NULL is Kitchen's
+ * one-tensor rms_rope1 (backend_rope.rs:364-440, "x", "scale"): only q is
+ * processed and k_scale, k_out are ignored. */
 int w8a8_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
                   void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
                   int64_t x_row_stride, int freq_per_batch, double eps, int dtype, hipStream_t stream);
+
+/* RoPE rotation alone: Kitchen's apply_rope (xq, xk) and, with k == NULL,
+ * apply_rope1 (x), native call inference/src/backend_rope.rs:256-299 with the
+ * numerics of the eager route (eager_apply :146-159, non-split):
+ *   out[2i + j] = T(f[i][j][0] * x[2i] + f[i][j][1] * x[2i + 1])   (fp32)
+ * Layouts, strides and freqs as for w8a8_rms_rope; outputs packed. */
+int w8a8_apply_rope(const void* x, const void* k, const float* freqs, void* out, void* k_out, int64_t batch,
+                    int64_t seq, int64_t heads, int64_t d, int64_t x_row_stride, int freq_per_batch, int dtype,
+                    hipStream_t stream);
 
 /* Gated residual of the DiT block (inference/src/models/qwen_image21/
  * numeric.rs:110-125): x, y [batch, tokens, d], gates [batch, d];

@@ -190,3 +190,9 @@ def test_rms_rope_host_errors():
                              None) == _lib.ERR_VALUE                  # null pointers
     assert lib.w8a8_rms_rope(None, None, None, None, None, None, None, 1, 4, 2, 8, 15, 0, 1e-6, _lib.BF16,
                              None) == _lib.ERR_VALUE                  # token rows overlap
+    assert lib.w8a8_apply_rope(None, None, None, None, None, 1, 4, 2, 7, 14, 0, _lib.BF16, None) == _lib.ERR_VALUE
+    assert lib.w8a8_apply_rope(None, None, None, None, None, 0, 4, 2, 8, 16, 0, _lib.BF16, None) == _lib.OK
+    assert lib.w8a8_apply_rope(None, None, None, None, None, 1, 4, 2, 8, 16, 0, _lib.BF16, None) == _lib.ERR_VALUE
+    assert lib.w8a8_apply_rope(None, None, None, None, None, 1, 4, 2, 8, 16, 0, 9, None) == _lib.ERR_RUNTIME
+    with pytest.raises(RuntimeError):
+        W.apply_rope1(q, torch.zeros(1, 4, 1, 4, 2, 2))                 # CPU tensors

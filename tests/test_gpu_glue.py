@@ -269,3 +269,35 @@ def test_rms_rope_pair_kernel_fp32_and_unaligned(case):
         mag = (m[..., 0::2].abs() + m[..., 1::2].abs()).repeat_interleave(2, -1).numpy()
         close(storage(got, dtype), storage(want, dtype), dtype, frac=0.0 if dtype == "f32" else 0.97,
               before_add=mag)
+
+
+@pytest.mark.parametrize("op", ["apply_rope", "apply_rope1", "rms_rope1"])
+@pytest.mark.parametrize("D", [128, 96])
+def test_rope_family_matches_eager_sequence(op, D):
+    """The rotation alone (apply_rope / apply_rope1) and the one-tensor
+    rms_rope1 against the eager route on the CPU: two ulps of the rotated
+    pair's magnitude and at least 97% bit-equal (the fp32 product sum may be
+    contracted to an fma on either side); the 16-byte-per-lane (D = 128) and
+    pair-per-lane (D = 96) kernels."""
+    g = torch.Generator().manual_seed(71)
+    B, S, H = 2, 150, 6
+    x = (torch.randn(B, S, H, D, generator=g) * 2).to(torch.bfloat16)
+    k = (torch.randn(B, S, H, D, generator=g) * 0.5).to(torch.bfloat16)
+    sc = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    f = _freqs(2, S, D, seed=72)
+    fd = f.to(DEV)
+    if op == "apply_rope":
+        got = W.apply_rope(x.to(DEV), k.to(DEV), fd)
+        want = (E.rope_apply(x, f), E.rope_apply(k, f))
+    elif op == "apply_rope1":
+        got = (W.apply_rope1(x.to(DEV), fd),)
+        want = (E.rope_apply(x, f),)
+    else:
+        got = (W.rms_rope1(x.to(DEV), fd, sc.to(DEV), 1e-6),)
+        want = (E.rms_rope(x, x, f, sc, sc, 1e-6)[0],)
+    for a, b, src in zip(got, want, (x, k)):
+        assert a.is_contiguous()
+        m = torch.nn.functional.rms_norm(src, (D,), sc, 1e-6) if op == "rms_rope1" else src
+        m = m.float()
+        mag = (m[..., 0::2].abs() + m[..., 1::2].abs()).repeat_interleave(2, -1).numpy()
+        close(storage(a, "bf16"), storage(b, "bf16"), "bf16", before_add=mag)
