@@ -6,7 +6,8 @@ Drop-in for the reference crate's ``int8_linear`` operator
 """
 from . import _lib
 from .glue import (adaln, gated_residual, int8_linear_modulated, modulated_norm, modulated_norm_quant,
-                   quantize_rowwise_modulated, rms_rope, rms_rope1, apply_rope, apply_rope1)
+                   quantize_rowwise_modulated, rms_rope, rms_rope1, apply_rope, apply_rope1, rms_rope_, rms_rope1_,
+                   apply_rope_, apply_rope1_)
 from .ops import (apply_residual, convrot_rotate, dequantize_linear, gemm_dequant, gemm_dequant_residual,
                   gemm_dequant_xq, gemm_i32, gemv_dequant, gemv_dequant_residual, int8_linear,
                   quantize_convrot_weight, quantize_rowwise, quantize_rowwise_convrot, quantize_tensorwise, route,
@@ -15,5 +16,5 @@ from .ops import (apply_residual, convrot_rotate, dequantize_linear, gemm_dequan
 __all__ = ["int8_linear", "quantize_rowwise", "row_scales", "gemv_dequant", "gemv_dequant_residual",
            "gemm_dequant", "gemm_dequant_residual", "gemm_dequant_xq", "gemm_i32", "dequantize_linear",
            "apply_residual", "convrot_rotate", "quantize_rowwise_convrot", "quantize_tensorwise",
-           "quantize_convrot_weight", "route", "adaln", "modulated_norm", "modulated_norm_quant", "gated_residual", "rms_rope", "rms_rope1", "apply_rope", "apply_rope1", "int8_linear_modulated",
+           "quantize_convrot_weight", "route", "adaln", "modulated_norm", "modulated_norm_quant", "gated_residual", "rms_rope", "rms_rope1", "apply_rope", "apply_rope1", "rms_rope_", "rms_rope1_", "apply_rope_", "apply_rope1_", "int8_linear_modulated",
            "quantize_rowwise_modulated", "_lib"]

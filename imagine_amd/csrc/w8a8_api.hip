@@ -123,6 +123,8 @@ int rope_entry(const char* name, const void* q, const void* k, const float* freq
     if (x_row_stride < heads * d) return fail(W8A8_ERR_VALUE, n + ": x_row_stride must be at least heads * d");
     if (!q || !freqs || !q_out || (norm && !q_scale)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
     if (k && (!k_out || (norm && !k_scale))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (k && ((q_out == q) != (k_out == k)))
+        return fail(W8A8_ERR_VALUE, n + ": both outputs equal their inputs (in place) or neither does");
     if (reinterpret_cast<uintptr_t>(freqs) % 16 != 0) return fail(W8A8_ERR_VALUE, "freqs must be 16-byte aligned");
     if (2 * batch * seq > 0x7fffffffll * 4) return fail(W8A8_ERR_VALUE, n + ": too many tokens");
     if (!w8a8::launch_rms_rope(q, k, freqs, q_scale, k ? k_scale : nullptr, q_out, k ? k_out : nullptr, batch, seq,

@@ -314,7 +314,11 @@ __global__ __launch_bounds__(NT) void modnorm_quant_rows_vec(
 // written as one 2-element access (row bases aligned to two elements).
 // NORM = false is the rotation alone (Kitchen's apply_rope / apply_rope1, the
 // eager route backend_rope.rs:146-159): m = x, exact in fp32.  k == nullptr
-// (ntensors = 1) is the one-tensor form (rms_rope1 / apply_rope1).
+// (ntensors = 1) is the one-tensor form (rms_rope1 / apply_rope1).  Output
+// tokens are o_stride elements apart: heads * d (packed), or x_stride for
+// the in-place forms (outputs equal to the inputs; every lane reads a group
+// of rows into registers before it writes the same elements, and groups are
+// disjoint).
 constexpr int kHeadGroup = 8;
 
 template <int DT, bool PAIR>
@@ -355,7 +359,8 @@ __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ 
                                                        const void* __restrict__ k_scale, void* __restrict__ q_out,
                                                        void* __restrict__ k_out, int64_t tokens, int64_t seq,
                                                        int64_t heads, int64_t d, int64_t x_stride,
-                                                       int ntensors, int freq_per_batch, float eps) {
+                                                       int64_t o_stride, int ntensors, int freq_per_batch,
+                                                       float eps) {
     using D = DType<DT>;
     using OS = typename D::storage;
     const int lane = threadIdx.x % kWave;
@@ -365,7 +370,7 @@ __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ 
     const int64_t tok = is_k ? wave - tokens : wave;
     const OS* x = static_cast<const OS*>(is_k ? k : q) + tok * x_stride;
     const OS* w = static_cast<const OS*>(is_k ? k_scale : q_scale);
-    OS* o = static_cast<OS*>(is_k ? k_out : q_out) + tok * heads * d;
+    OS* o = static_cast<OS*>(is_k ? k_out : q_out) + tok * o_stride;
     const int64_t b = tok / seq, t = tok % seq;
     const float4* f = reinterpret_cast<const float4*>(freqs + ((freq_per_batch ? b * seq : 0) + t) * (d / 2) * 4);
     float4 fv[PPL];
@@ -436,8 +441,8 @@ __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restric
                                                            const void* __restrict__ k_scale,
                                                            void* __restrict__ q_out, void* __restrict__ k_out,
                                                            int64_t tokens, int64_t seq, int64_t heads,
-                                                           int64_t x_stride, int ntensors, int freq_per_batch,
-                                                           float eps) {
+                                                           int64_t x_stride, int64_t o_stride, int ntensors,
+                                                           int freq_per_batch, float eps) {
     using D = DType<DT>;
     using OS = typename D::storage;
     static_assert(sizeof(OS) == 2, "16-bit rows only");
@@ -449,7 +454,7 @@ __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restric
     const int64_t tok = is_k ? wave - tokens : wave;
     const int sub = lane / LPR, col = lane % LPR;
     const OS* x = static_cast<const OS*>(is_k ? k : q) + tok * x_stride + col * 8;
-    OS* o = static_cast<OS*>(is_k ? k_out : q_out) + tok * heads * d + col * 8;
+    OS* o = static_cast<OS*>(is_k ? k_out : q_out) + tok * o_stride + col * 8;
     const int64_t b = tok / seq, t = tok % seq;
     const float4* f = reinterpret_cast<const float4*>(freqs + ((freq_per_batch ? b * seq : 0) + t) * (d / 2) * 4) +
                       col * 4;
@@ -744,6 +749,7 @@ bool launch_rms_rope(const void* q, const void* k, const float* freqs, const voi
                      hipStream_t stream) {
     const int64_t tokens = batch * seq;
     const int nt = k ? 2 : 1;
+    const int64_t o_stride = q_out == q ? x_stride : heads * d;
     const dim3 grid(static_cast<unsigned>((nt * tokens + 3) / 4)), block(256);
     const int fpb = freq_per_batch ? 1 : 0;
     const int ppl = d <= 128 ? 1 : d <= 256 ? 2 : 0;
@@ -751,7 +757,7 @@ bool launch_rms_rope(const void* q, const void* k, const float* freqs, const voi
     const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (dtype != W8A8_F32 && (d == 64 || d == 128 || d == 256) && x_stride % 8 == 0 && a16(q) && a16(k) &&
         a16(q_out) && a16(k_out) && a16(q_scale) && a16(k_scale)) {
-#define W8A8_RV_N(DT, LPR, N) hipLaunchKernelGGL((rms_rope_tokens_vec<DT, LPR, N>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, x_stride, nt, fpb, eps)
+#define W8A8_RV_N(DT, LPR, N) hipLaunchKernelGGL((rms_rope_tokens_vec<DT, LPR, N>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, x_stride, o_stride, nt, fpb, eps)
 #define W8A8_RV(DT, LPR) do { if (norm) W8A8_RV_N(DT, LPR, true); else W8A8_RV_N(DT, LPR, false); } while (0)
 #define W8A8_RV_D(DT) do { if (d == 64) W8A8_RV(DT, 8); else if (d == 128) W8A8_RV(DT, 16); else W8A8_RV(DT, 32); } while (0)
         if (dtype == W8A8_BF16) W8A8_RV_D(W8A8_BF16);
@@ -765,7 +771,7 @@ bool launch_rms_rope(const void* q, const void* k, const float* freqs, const voi
     const bool pair = x_stride % 2 == 0 && reinterpret_cast<uintptr_t>(q) % al == 0 &&
                       reinterpret_cast<uintptr_t>(k) % al == 0 && reinterpret_cast<uintptr_t>(q_out) % al == 0 &&
                       reinterpret_cast<uintptr_t>(k_out) % al == 0;
-#define W8A8_RR_N(DT, PPL, PAIR, N) hipLaunchKernelGGL((rms_rope_tokens<DT, PPL, PAIR, N>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, d, x_stride, nt, fpb, eps)
+#define W8A8_RR_N(DT, PPL, PAIR, N) hipLaunchKernelGGL((rms_rope_tokens<DT, PPL, PAIR, N>), grid, block, 0, stream, q, k, freqs, q_scale, k_scale, q_out, k_out, tokens, seq, heads, d, x_stride, o_stride, nt, fpb, eps)
 #define W8A8_RR(DT, PPL, PAIR) do { if (norm) W8A8_RR_N(DT, PPL, PAIR, true); else W8A8_RR_N(DT, PPL, PAIR, false); } while (0)
 #define W8A8_RR_P(DT, PPL) do { if (pair) W8A8_RR(DT, PPL, true); else W8A8_RR(DT, PPL, false); } while (0)
 #define W8A8_RR_D(DT) do { if (ppl == 1) W8A8_RR_P(DT, 1); else W8A8_RR_P(DT, 2); } while (0)

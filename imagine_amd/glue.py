@@ -200,7 +200,7 @@ def modulated_norm_quant(x, scale, prefix, shift, eps, rms=False, *, scale_form=
     return q, s
 
 
-def _rope(name, q, k, freqs_cis, q_scale, k_scale, epsilon, norm):
+def _rope(name, q, k, freqs_cis, q_scale, k_scale, epsilon, norm, inplace=False):
     """Checks, layout and launch shared by the non-split RoPE family; k None
     is the one-tensor form.  Returns packed (q_out, k_out or None)."""
     _require_cuda(*[t for t in (q, k, freqs_cis, q_scale) if t is not None])
@@ -216,12 +216,17 @@ def _rope(name, q, k, freqs_cis, q_scale, k_scale, epsilon, norm):
         raise RuntimeError(f"{name}: the second tensor and the scales must have the dtype of the first")
     rs = q.stride(1)
     if q.stride() != (s * rs, rs, d, 1) or (k is not None and k.stride() != q.stride()) or rs < h * d:
+        if inplace:
+            raise NotImplementedError(f"{name}: in place on this stride layout is not part of this build")
         q = q.contiguous()
         k = None if k is None else k.contiguous()
         rs = h * d
     f = freqs_cis.contiguous()
-    qo = torch.empty((b, s, h, d), device=q.device, dtype=q.dtype)
-    ko = None if k is None else torch.empty_like(qo)
+    if inplace:
+        qo, ko = q, k
+    else:
+        qo = torch.empty((b, s, h, d), device=q.device, dtype=q.dtype)
+        ko = None if k is None else torch.empty_like(qo)
     fpb = 1 if fs[0] == b and b > 1 else 0
     code = _dtype_code(q.dtype, name)
     if norm:
@@ -268,3 +273,27 @@ def apply_rope1(x, freqs_cis):
     """Kitchen's ``apply_rope1`` (the DiT's attention-patch route,
     models/qwen_image21/dit.rs:460-480): ``apply_rope`` on one tensor."""
     return _rope("apply_rope1", x, None, freqs_cis, None, None, 0.0, False)[0]
+
+
+def rms_rope_(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6):
+    """Kitchen's in-place ``rms_rope_``: ``rms_rope`` written back over q and
+    k (views into a QKV output included).  Returns (q, k)."""
+    return _rope("rms_rope_", q, k, freqs_cis, q_scale, q_scale if k_scale is None else k_scale, epsilon, True,
+                 inplace=True)
+
+
+def rms_rope1_(x, freqs_cis, scale, epsilon=1e-6):
+    """Kitchen's in-place ``rms_rope1_``.  Returns x."""
+    return _rope("rms_rope1_", x, None, freqs_cis, scale, None, epsilon, True, inplace=True)[0]
+
+
+def apply_rope_(xq, xk, freqs_cis):
+    """Kitchen's in-place ``apply_rope_``.  Returns (xq, xk)."""
+    if xk is None:
+        raise RuntimeError("apply_rope_: xk is required (apply_rope1_ takes one tensor)")
+    return _rope("apply_rope_", xq, xk, freqs_cis, None, None, 0.0, False, inplace=True)
+
+
+def apply_rope1_(x, freqs_cis):
+    """Kitchen's in-place ``apply_rope1_``.  Returns x."""
+    return _rope("apply_rope1_", x, None, freqs_cis, None, None, 0.0, False, inplace=True)[0]

@@ -273,7 +273,10 @@ int w8a8_modulated_norm_quant(const void* x, const void* scale0, const void* sca
  *   out[2i + j] = T(f[i][j][0] * m[2i] + f[i][j][1] * m[2i + 1])   (fp32)
  * d even, at most 256; x_row_stride >= heads * d.  k == NULL is Kitchen's
  * one-tensor rms_rope1 (backend_rope.rs:364-440, "x", "scale"): only q is
- * processed and k_scale, k_out are ignored. */
+ * processed and k_scale, k_out are ignored.  q_out == q and k_out == k (both
+ * or neither) are the in-place forms (rms_rope_, rms_rope1_): the outputs then
+ * keep the inputs' token stride; other overlaps of inputs and outputs are not
+ * allowed. */
 int w8a8_rms_rope(const void* q, const void* k, const float* freqs, const void* q_scale, const void* k_scale,
                   void* q_out, void* k_out, int64_t batch, int64_t seq, int64_t heads, int64_t d,
                   int64_t x_row_stride, int freq_per_batch, double eps, int dtype, hipStream_t stream);
@@ -282,7 +285,8 @@ int w8a8_rms_rope(const void* q, const void* k, const float* freqs, const void* 
  * apply_rope1 (x), native call inference/src/backend_rope.rs:256-299 with the
  * numerics of the eager route (eager_apply :146-159, non-split):
  *   out[2i + j] = T(f[i][j][0] * x[2i] + f[i][j][1] * x[2i + 1])   (fp32)
- * Layouts, strides and freqs as for w8a8_rms_rope; outputs packed. */
+ * Layouts, strides, freqs and the in-place forms (apply_rope_, apply_rope1_:
+ * out == x) as for w8a8_rms_rope; other outputs packed. */
 int w8a8_apply_rope(const void* x, const void* k, const float* freqs, void* out, void* k_out, int64_t batch,
                     int64_t seq, int64_t heads, int64_t d, int64_t x_row_stride, int freq_per_batch, int dtype,
                     hipStream_t stream);

@@ -196,3 +196,7 @@ def test_rms_rope_host_errors():
     assert lib.w8a8_apply_rope(None, None, None, None, None, 1, 4, 2, 8, 16, 0, 9, None) == _lib.ERR_RUNTIME
     with pytest.raises(RuntimeError):
         W.apply_rope1(q, torch.zeros(1, 4, 1, 4, 2, 2))                 # CPU tensors
+    # q written in place but k not: refused before anything is launched or read
+    assert lib.w8a8_rms_rope(4096, 8192, 12288, 16384, 16384, 4096, 20480, 1, 4, 2, 8, 16, 0, 1e-6, _lib.BF16,
+                             None) == _lib.ERR_VALUE
+    assert "in place" in lib.w8a8_last_error().decode()

@@ -301,3 +301,39 @@ def test_rope_family_matches_eager_sequence(op, D):
         m = m.float()
         mag = (m[..., 0::2].abs() + m[..., 1::2].abs()).repeat_interleave(2, -1).numpy()
         close(storage(a, "bf16"), storage(b, "bf16"), "bf16", before_add=mag)
+
+
+@pytest.mark.parametrize("op", ["rms_rope_", "apply_rope1_"])
+def test_rope_in_place_forms(op):
+    """The in-place forms write the eager route's result back over their
+    inputs: rms_rope_ on q / k views into one [B, S, 3, H, 128] QKV output
+    (the v third untouched; 16-byte-per-lane kernel), apply_rope1_ on a packed
+    [B, S, H, 96] tensor (pair-per-lane kernel)."""
+    g = torch.Generator().manual_seed(81)
+    B, S, H = 2, 150, 6
+    if op == "rms_rope_":
+        D = 128
+        qkv = (torch.randn(B, S, 3, H, D, generator=g) * 1.5).to(torch.bfloat16)
+        sc = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+        f = _freqs(1, S, D, seed=82)
+        qkv_d = qkv.to(DEV)
+        rq, rk = W.rms_rope_(qkv_d[:, :, 0], qkv_d[:, :, 1], f.to(DEV), sc.to(DEV), sc.to(DEV), 1e-6)
+        assert rq.data_ptr() == qkv_d[:, :, 0].data_ptr() and rk.data_ptr() == qkv_d[:, :, 1].data_ptr()
+        q, k = qkv[:, :, 0].contiguous(), qkv[:, :, 1].contiguous()
+        wq, wk = E.rms_rope(q, k, f, sc, sc, 1e-6)
+        got = qkv_d.cpu()
+        assert torch.equal(got[:, :, 2], qkv[:, :, 2])
+        pairs = ((got[:, :, 0], wq, q), (got[:, :, 1], wk, k))
+    else:
+        D = 96
+        x = (torch.randn(B, S, H, D, generator=g) * 2).to(torch.bfloat16)
+        sc = None
+        f = _freqs(2, S, D, seed=83)
+        xd = x.to(DEV)
+        r = W.apply_rope1_(xd, f.to(DEV))
+        assert r.data_ptr() == xd.data_ptr()
+        pairs = ((xd.cpu(), E.rope_apply(x, f), x),)
+    for a, b, src in pairs:
+        m = (torch.nn.functional.rms_norm(src, (D,), sc, 1e-6) if sc is not None else src).float()
+        mag = (m[..., 0::2].abs() + m[..., 1::2].abs()).repeat_interleave(2, -1).numpy()
+        close(storage(a, "bf16"), storage(b, "bf16"), "bf16", before_add=mag)
