@@ -257,10 +257,7 @@ def main():
 def traffic_bytes():
     """HBM bytes per launch of the roofline kernel, read from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the same kernel and workload
-    (profiles/), or None when a tuning knob selects another main loop than the
-    one profiled."""
-    if os.environ.get("W8A8_GEMM_MAINLOOP") or os.environ.get("W8A8_GEMM_GLOBAL_LOADS"):
-        return None
+    (profiles/)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         "hbm_traffic_ffn_up_gemm_and_quant_M11712.txt")
     key = "gemm_mfma_dma DmaCfg<256,256,128,64,128,2,2> ffn_up traffic_bytes_per_launch:"

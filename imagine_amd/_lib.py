@@ -16,6 +16,14 @@ OUT_INT32 = 1 << 2
 FUSED_QUANT = 1 << 3
 ROUTE_GEMM = 1 << 4
 GIVEN_SCALE = 1 << 5
+# GEMM main loops (flag bits 8..11: GEMM_TILE(code))
+TILE_AUTO, TILE_256x192, TILE_256x256, TILE_384x192, TILE_256x128, TILE_REGS, TILE_GENERIC = range(7)
+TILE_NAMES = {TILE_AUTO: "auto", TILE_256x192: "256x192", TILE_256x256: "256x256", TILE_384x192: "384x192",
+              TILE_256x128: "256x128", TILE_REGS: "regs", TILE_GENERIC: "generic"}
+
+
+def GEMM_TILE(code):
+    return code << 8
 
 # Every symbol include/w8a8.h declares, with (restype, argtypes).
 _p, _i, _i64, _u32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32
@@ -27,6 +35,7 @@ SIGNATURES = {
     "w8a8_row_scales": (_i, [_p, _i, _p, _i64, _i64, _u32, _p]),
     "w8a8_gemv_dequant": (_i, [_p, _p, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _u32, _p]),
     "w8a8_gemm_dequant": (_i, [_p, _p, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _u32, _p]),
+    "w8a8_gemm_config": (_i, [_i64, _i64, _i64, _u32]),
     "w8a8_gemm_dequant_xq": (_i, [_p, _i, _p, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _u32, _p]),
     "w8a8_dequantize_linear": (_i, [_p, _p, _p, _i64, _p, _p, _i, _i64, _i64, _u32, _p]),
     "w8a8_int8_linear_workspace_bytes": (_i64, [_i64, _i64]),

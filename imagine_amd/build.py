@@ -3,6 +3,8 @@
     python -m imagine_amd.build            # or: python imagine_amd/build.py
 
 Each .hip source compiles to its own object in parallel, then one link.
+The GELU lookup tables (imagine_amd/gelu_tables.py) are generated into the
+build directory first.
 Flags: -O3, IEEE float (no fast-math; contractions only where fmaf is
 written), packed-fp32 instructions disabled.
 """
@@ -18,8 +20,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libw8a8_hip.so"
-SOURCES = ["w8a8_quant.hip", "w8a8_convrot.hip", "w8a8_gemv.hip", "w8a8_gemm.hip", "w8a8_glue.hip",
-           "w8a8_api.hip"]
+SOURCES = ["w8a8_gemm_f32.hip", "w8a8_gemm_bf16.hip", "w8a8_gemm_f16.hip", "w8a8_gemm.hip", "w8a8_quant.hip",
+           "w8a8_glue.hip", "w8a8_convrot.hip", "w8a8_gemv.hip", "w8a8_api.hip"]
 ARCH = os.environ.get("W8A8_OFFLOAD_ARCH", "gfx950")
 
 
@@ -41,9 +43,14 @@ def flags():
 def build(verbose=False, extra=()):
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="w8a8_build_") as tmp:
+        # generated sources: the GELU lookup tables
+        sys.path.insert(0, str(ROOT))
+        from imagine_amd import gelu_tables
+        (Path(tmp) / "w8a8_gelu_tables.h").write_text(gelu_tables.header_text())
+
         def compile_one(src):
             obj = Path(tmp) / (Path(src).stem + ".o")
-            cmd = [cc, *flags(), *extra, "-c", str(CSRC / src), "-o", str(obj)]
+            cmd = [cc, *flags(), f"-I{tmp}", *extra, "-c", str(CSRC / src), "-o", str(obj)]
             r = subprocess.run(cmd, capture_output=True, text=True)
             noise = "is not a recognized feature for this target"
             err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)

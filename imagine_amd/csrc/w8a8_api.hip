@@ -18,7 +18,8 @@ void launch_gemv(const int8_t* q, const int8_t* w, const float* xs, const float*
                  int64_t M, int64_t N, int64_t K, bool gelu, hipStream_t stream);
 void launch_gemm(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                  int64_t ws_size, const void* bias, const Residual* res, void* out, int out_dtype,
-                 int64_t M, int64_t N, int64_t K, bool gelu, bool int32_out, hipStream_t stream);
+                 int64_t M, int64_t N, int64_t K, bool gelu, bool int32_out, int tile, hipStream_t stream);
+int gemm_config(int64_t M, int64_t N, int64_t K, int requested);
 void launch_residual(void* out, const void* resid, const void* rscale, int64_t rs_size, int dtype,
                      int64_t M, int64_t N, hipStream_t stream);
 bool launch_gemm_xq(const void* x, int x_dtype, const float* xs, const int8_t* w, const float* ws,
@@ -73,7 +74,14 @@ int check_launch(const char* what) {
 bool valid_dtype(int d) { return d == W8A8_F32 || d == W8A8_F16 || d == W8A8_BF16; }
 
 constexpr uint32_t kKnownFlags = W8A8_SCALE_RECIP | W8A8_ACT_GELU_TANH | W8A8_OUT_INT32 |
-                                 W8A8_FUSED_QUANT | W8A8_ROUTE_GEMM | W8A8_GIVEN_SCALE;
+                                 W8A8_FUSED_QUANT | W8A8_ROUTE_GEMM | W8A8_GIVEN_SCALE | W8A8_GEMM_TILE_MASK;
+
+int tile_of(uint32_t flags) { return static_cast<int>((flags & W8A8_GEMM_TILE_MASK) >> W8A8_GEMM_TILE_SHIFT); }
+
+int check_tile(uint32_t flags) {
+    if (tile_of(flags) > W8A8_GEMM_TILE_GENERIC) return fail(W8A8_ERR_VALUE, "unknown W8A8_GEMM_TILE code");
+    return W8A8_OK;
+}
 
 int check_common(int64_t M, int64_t N, int64_t K, uint32_t flags) {
     if (M < 0 || N < 0 || K < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
@@ -279,11 +287,17 @@ int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const f
     if (!i32) {
         if (int rc = check_ws(ws_size, N, "INT8 weight scale must be scalar or per-output-channel")) return rc;
     }
+    if (int rc = check_tile(flags)) return rc;
     if (M == 0 || N == 0) return W8A8_OK;
     if (!out || (K > 0 && (!q || !w)) || (!i32 && (!xs || !ws))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
     w8a8::launch_gemm(q, w, xs, ws, ws_size, bias, nullptr, out, i32 ? W8A8_F32 : out_dtype, M, N, K,
-                      flags & W8A8_ACT_GELU_TANH, i32, stream);
+                      flags & W8A8_ACT_GELU_TANH, i32, tile_of(flags), stream);
     return check_launch("int8_gemm_dequant");
+}
+
+int w8a8_gemm_config(int64_t M, int64_t N, int64_t K, uint32_t flags) {
+    if (M < 0 || N < 0 || K < 0 || (flags & ~kKnownFlags) || tile_of(flags) > W8A8_GEMM_TILE_GENERIC) return -1;
+    return w8a8::gemm_config(M, N, K, tile_of(flags));
 }
 
 int w8a8_gemm_dequant_residual(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
@@ -296,10 +310,12 @@ int w8a8_gemm_dequant_residual(const int8_t* q, const int8_t* w, const float* xs
     if (!valid_dtype(out_dtype)) return fail(W8A8_ERR_RUNTIME, "Invalid INT8 linear output dtype code");
     if (int rc = check_ws(ws_size, N, "INT8 weight scale must be scalar or per-output-channel")) return rc;
     if (int rc = check_residual(rscale, rscale_size, resid, N)) return rc;
+    if (int rc = check_tile(flags)) return rc;
     if (M == 0 || N == 0) return W8A8_OK;
     if (!out || !xs || !ws || (K > 0 && (!q || !w))) return fail(W8A8_ERR_VALUE, "null tensor pointer");
     const w8a8::Residual res{rscale, rscale_size, resid};
-    w8a8::launch_gemm(q, w, xs, ws, ws_size, bias, &res, out, out_dtype, M, N, K, false, false, stream);
+    w8a8::launch_gemm(q, w, xs, ws, ws_size, bias, &res, out, out_dtype, M, N, K, false, false, tile_of(flags),
+                      stream);
     return check_launch("cutlass_int8_dequant_residual");
 }
 

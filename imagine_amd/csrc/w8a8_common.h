@@ -10,7 +10,8 @@
 
 #include <type_traits>
 
-#include "../../include/w8a8.h"
+#include "w8a8.h"
+#include "w8a8_gelu_tables.h"  // generated at build time (imagine_amd/gelu_tables.py)
 
 namespace w8a8 {
 
@@ -93,50 +94,81 @@ template <> struct DType<W8A8_BF16> {
 // ---------------------------------------------------------------- GELU (tanh)
 
 // gelu_tanh(x) = 0.5 * x * (1 + tanh(u)),  u = sqrt(2/pi) * (x + 0.044715 * x^3),
-// the reference's input_act "gelu_tanh" (inference/src/int8_linear.rs:37-41),
-// in ATen's operation order.  1 + tanh(u) is formed in fp32 exactly as the
-// reference forms it, so the cancellation of its negative tail matches.  Only
-// tanh itself is evaluated differently, from t = exp(-2|u|) (hardware exp2 and
-// reciprocal, about 1 ulp each): tanh(|u|) = 1 - 2t / (1 + t) for |u| >= 0.55,
-// where the error falls on the small term and the result is the correctly
-// rounded tanh up to rounding ties, and (1 - t) / (1 + t) below (absolute
-// error about 2^-24).
-__device__ __forceinline__ float tanh_fast(float u) {
-    const float kMinus2Log2e = -2.88539008177792681472f;  // -2 / ln(2)
-    const float a = fabsf(u);
-    const float t = __builtin_amdgcn_exp2f(a * kMinus2Log2e);  // (0, 1]
-    const float rc = __builtin_amdgcn_rcpf(1.0f + t);
-    const float r = a >= 0.55f ? 1.0f - (2.0f * t) * rc : (1.0f - t) * rc;
-    return __builtin_copysignf(r, u);
+// the reference's input_act "gelu_tanh" (inference/src/int8_linear.rs:37-41):
+// ATen's operation order in fp32, tanh correctly rounded to fp32.
+//
+// A 16-bit input has 65536 values, so 16-bit GELU is a lookup: the tables of
+// w8a8_gelu_tables.h (generated at build time by imagine_amd/gelu_tables.py,
+// which checks its closed forms on every pattern) hold the rounded result for
+// the inputs where it is not one of the closed forms below.  Exact by
+// construction; every pattern is compared with the oracle on the GPU.
+
+// bf16 pattern b (low 16 bits) -> bf16 pattern of gelu_tanh(b).  tab has the
+// kGeluBf16Table layout and may be that global table or an LDS copy.  Written
+// without branches: the table is read at a clamped (always valid) index and
+// the closed forms are selected afterwards, so a run of lookups issues its
+// reads back to back instead of waiting on each one.
+__device__ __forceinline__ uint32_t gelu_bf16_bits(uint32_t b, const uint16_t* tab) {
+    const uint32_t a = b & 0x7fffu;
+    const uint32_t ac = a < kGeluBf16Lo ? kGeluBf16Lo : (a >= kGeluBf16Hi ? kGeluBf16Hi - 1 : a);
+    const uint32_t looked = tab[(b >> 15) * kGeluBf16Span + (ac - kGeluBf16Lo)];
+    const uint32_t half = f32_to_bf16(0.5f * bf16_to_f32(static_cast<uint16_t>(b)));  // 1 + tanh(u) rounds away
+    const uint32_t neg_big = a == 0x7f80u ? 0xffc0u : 0x8000u;     // -inf: 0 * -inf; finite: -0
+    uint32_t big = (b & 0x8000u) ? neg_big : b;                     // tanh(u) = 1: x
+    big = a > 0x7f80u ? (b | 0x40u) : big;                          // NaN: the input, quieted
+    return a < kGeluBf16Lo ? half : (a >= kGeluBf16Hi ? big : looked);
 }
 
-__device__ __forceinline__ float gelu_tanh(float x) {
+// fp16 pattern b -> fp16 pattern of gelu_tanh(b); the table covers |x| < 6.
+__device__ __forceinline__ uint32_t gelu_f16_bits(uint32_t b, const uint16_t* tab) {
+    const uint32_t a = b & 0x7fffu;
+    if (a >= kGeluF16Hi) {
+        if (a > 0x7c00u) return b | 0x200u;
+        if (b & 0x8000u) return a == 0x7c00u ? 0xfe00u : 0x8000u;
+        return b;
+    }
+    return tab[(b >> 15) * kGeluF16Span + a];
+}
+
+// fp32 input: evaluated, with tanh from the double-precision tanh of the fp32
+// argument rounded once (the correctly rounded fp32 tanh in all but
+// vanishingly rare cases).
+__device__ __forceinline__ float gelu_f32(float x) {
     const float kBeta = 0.79788456080286535588f;  // sqrt(2) * (2/sqrt(pi)) * 0.5
     const float kKappa = 0.044715f;
-    float x_cube = x * x * x;
-    float inner = kBeta * (x + kKappa * x_cube);
-    return 0.5f * x * (1.0f + tanh_fast(inner));
+    const float x_cube = x * x * x;
+    const float inner = kBeta * (x + kKappa * x_cube);
+    const float t = static_cast<float>(tanh(static_cast<double>(inner)));
+    return 0.5f * x * (1.0f + t);
 }
 
-// GELU-tanh of an epilogue output (rounded to a 16-bit output afterwards,
-// where one ulp of slack is allowed), in the reference's structure
-// 0.5 x (1 + tanh(u)) but with fewer operations than gelu_tanh:
+// GELU of the 16-bit pattern b of dtype DT (global tables).
+template <int DT>
+__device__ __forceinline__ uint32_t gelu_bits(uint32_t b) {
+    static_assert(DT != W8A8_F32, "16-bit dtypes only");
+    if constexpr (DT == W8A8_BF16) return gelu_bf16_bits(b, kGeluBf16Table);
+    else return gelu_f16_bits(b, kGeluF16Table);
+}
+
+// The fused GEMM epilogue's GELU (the LDS-staged bf16 path of FFN-up): an
+// evaluation in fewer operations than a lookup, within one bf16 ulp of the
+// exact result and equal to it on all but about 0.1% of inputs.  A branchless
+// LDS copy of the bf16 table measured 12% slower on the whole FFN-up GEMM
+// (11712 x 3072 x 12288: 498 vs 442 us), the global table 18%: the epilogue
+// runs while the matrix cores idle, so its instruction count is what counts.
+// Structure 0.5 x (1 + tanh(u)) as the reference's:
 //   e = x (a + b x^2) = 2u / ln 2           (sqrt(2/pi) and 0.044715 pre-scaled
 //                                            by 2 / ln 2, so exp2 takes -|e|
 //                                            through its input modifiers; u
 //                                            has the sign of x)
 //   t = exp(-2|u|),  r = 1 - 2 t / (1 + t)  (|tanh u| as one fma; the
-//                                            subtraction rounds like the
-//                                            reference's fp32 tanh, so 1 + tanh u
-//                                            cancels as it does: exactly 0 once
-//                                            |u| > 9)
+//                                            subtraction rounds like an fp32
+//                                            tanh, so 1 + tanh u cancels as it
+//                                            does: exactly 0 once |u| > 9)
 //   gelu = (x/2) (1 + copysign(r, x))       (the reference's two roundings:
 //                                            a single fma would turn the -0 of
-//                                            the saturated negative tail into
-//                                            +0)
-// Near u = 0 r carries an absolute error of ~2^-24, which only moves the
-// 1 + tanh(u) term by an ulp.  The quantizer's input activation, whose int8
-// codes are compared bit for bit, keeps gelu_tanh.
+//                                            the saturated negative tail into +0)
+// exp2 and the reciprocal are the hardware approximations (about 1 ulp).
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
     const float kA = 2.302208198144325f;      // sqrt(2/pi) * 2 / ln 2
     const float kB = 0.1029432395800235f;     // sqrt(2/pi) * 0.044715 * 2 / ln 2
@@ -148,12 +180,9 @@ __device__ __forceinline__ float gelu_tanh_fast(float x) {
 }
 
 // Two bf16 pre-activations packed in one word (low half first) -> their
-// GELU-tanh, packed the same way.  Equal to rounding each input with
-// DType<bf16>::round and applying gelu_tanh_fast, with the pair rounded by one
-// v_cvt_pk_bf16_f32 on each side.
-__device__ __forceinline__ uint32_t gelu_bf16x2(uint32_t p) {
-    return pack2_bf16(gelu_tanh_fast(__uint_as_float(p << 16)),
-                      gelu_tanh_fast(__uint_as_float(p & 0xffff0000u)));
+// gelu_tanh_fast, rounded and packed the same way (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t gelu_bf16x2_fast(uint32_t p) {
+    return pack2_bf16(gelu_tanh_fast(__uint_as_float(p << 16)), gelu_tanh_fast(__uint_as_float(p & 0xffff0000u)));
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
@@ -279,12 +308,19 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
 
 // ---------------------------------------------------------------- epilogue
 
+// GELU of a value v already rounded to dtype T, as a float.
+template <int DT>
+__device__ __forceinline__ float gelu_value(float v) {
+    if constexpr (DT == W8A8_F32) return gelu_f32(v);
+    else return DType<DT>::load(static_cast<typename DType<DT>::storage>(gelu_bits<DT>(DType<DT>::store(v))));
+}
+
 // out = O( fma(float(acc) * xs, ws, bias) ), optional gelu on the O-rounded value.
 template <int ODT>
 __device__ __forceinline__ float epilogue_value(int acc, float xs, float ws, float bias, bool gelu) {
     float t = static_cast<float>(acc) * xs;
     float v = fmaf(t, ws, bias);
-    if (gelu) v = gelu_tanh_fast(DType<ODT>::round(v));
+    if (gelu) v = gelu_value<ODT>(DType<ODT>::round(v));
     return v;
 }
 

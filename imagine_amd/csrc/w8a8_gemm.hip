@@ -1,102 +1,16 @@
 // Host-side dispatch of the W8A8 GEMM kernels (w8a8_gemm_kernels.h): choice
-// of main loop and tile configuration, launch, and the C-ABI-facing launchers.
-#include <cstdlib>
-#include <cstring>
-
-#include "w8a8_gemm_kernels.h"
+// of main loop and tile configuration (gemm_config) and the C-ABI-facing
+// launchers.  The per-dtype instantiations of gemm_dispatch live in
+// w8a8_gemm_{bf16,f16,f32}.hip.
+#include "w8a8_gemm_launch.h"
 
 namespace w8a8 {
-
-// ------------------------------------------------------------------ host side
-
-constexpr int kBN = 256, kBM = 256, kBK = 64, kWN = 128, kWM = 128;
-constexpr int kGroupM = 4;
-
-constexpr Residual kNoResidual{nullptr, 0, nullptr};
-
-template <int ODT, int MODE, bool GELU, int XDT>
-static void launch_mfma(const int8_t* q, const void* x, const int8_t* w, const float* xs,
-                        const float* ws, int64_t ws_size, const void* bias, const Residual& res,
-                        void* out, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-    const int tiles = static_cast<int>(((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN));
-    hipLaunchKernelGGL((gemm_mfma<ODT, MODE, GELU, XDT, kBN, kBM, kBK, kWN, kWM>), dim3(tiles),
-                       dim3(256), 0, stream, q, x, w, xs, ws, ws_size, bias, res, out,
-                       static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), kGroupM);
-}
 
 bool gemm_mfma_supported(const void* a, size_t a_elem, const int8_t* w, int64_t M, int64_t N,
                          int64_t K) {
     return K % 16 == 0 && M < (1ll << 31) / 2 && N < (1ll << 31) / 2 &&
            reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
            M * K * static_cast<int64_t>(a_elem) < (1ll << 40);
-}
-
-// Main-loop configurations of the int8-input GEMM (weights BN x activations BM
-// per block, wave tile WN x WM, BK bytes per K tile, ring depth, waves per SIMD).
-//   N256M192W8: 8 waves of 64 x 96 on a 256 x 192 tile, 2-stage ring of
-//               128-byte K tiles (112 KB of LDS), one block per CU.  The
-//               default: 192-token tiles cut M = 11712 (2 x 5856) exactly and
-//               fill the 256 CUs in rounds that are ~95% full at N = 3072,
-//               9216 and 12288.
-//   N256M256W8: 8 waves of 128 x 64 on a 256 x 256 tile, 2-stage ring of
-//               128-byte K tiles (128 KB of LDS), one block per CU.
-//   N256M128:   4 waves of 128 x 64 on a 256 x 128 tile, 3-stage ring of 64-byte
-//               K tiles (72 KB), two blocks per CU.
-//   N256M256:   4 waves of 128 x 128, 2-stage ring of 128-byte tiles, one wave
-//               per SIMD.
-//   N384M192W8: 8 waves of 96 x 96 on a 384 x 192 tile, 2-stage ring of
-//               128-byte K tiles (144 KB of LDS, the staged output exactly
-//               fills it), one block per CU.
-using CfgN256M192W8 = DmaCfg<256, 192, 64, 96, 128, 2, 2>;
-using CfgN256M256W8 = DmaCfg<256, 256, 128, 64, 128, 2, 2>;
-using CfgN384M192W8 = DmaCfg<384, 192, 96, 96, 128, 2, 2>;
-using CfgN256M128 = DmaCfg<256, 128, 128, 64, 64, 3, 2>;
-using CfgN256M256 = DmaCfg<256, 256, 128, 128, 128, 2, 1>;
-
-// W8A8_GEMM_MAINLOOP = n256m192w8 | n256m256w8 | n384m192w8 | n256m128 | n256m256 | regs
-// forces one (a tuning knob; every choice produces identical results).  By
-// default the shape picks among N256M192W8, N256M256W8 and N384M192W8
-// (default_tile).
-static int mainloop_choice() {
-    static int choice = [] {
-        const char* e = std::getenv("W8A8_GEMM_MAINLOOP");
-        if (!e) return 5;
-        if (std::strcmp(e, "regs") == 0) return 0;
-        if (std::strcmp(e, "n256m128") == 0) return 1;
-        if (std::strcmp(e, "n256m256") == 0) return 3;
-        if (std::strcmp(e, "n256m256w8") == 0) return 4;
-        if (std::strcmp(e, "n256m192w8") == 0) return 6;
-        if (std::strcmp(e, "n384m192w8") == 0) return 7;
-        return 5;
-    }();
-    return choice;
-}
-
-// W8A8_GEMM_GLOBAL_LOADS=1 forces the global_load_lds form (tuning knob;
-// identical results).
-static bool buffer_loads_disabled() {
-    static bool off = [] {
-        const char* e = std::getenv("W8A8_GEMM_GLOBAL_LOADS");
-        return e && e[0] == '1';
-    }();
-    return off;
-}
-
-template <int ODT, int MODE, bool GELU, class C>
-static void launch_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                       int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
-                       int64_t N, int64_t K, hipStream_t stream) {
-    const int tiles = static_cast<int>(((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN));
-    // buffer-resource loads take 32-bit offsets: both operands below 2 GiB
-    const int64_t kBufLimit = (1ll << 31) - 4096;
-    if (M * K < kBufLimit && N * K < kBufLimit && !buffer_loads_disabled())
-        hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C, true>), dim3(tiles), dim3(C::kThreads), 0, stream,
-                           q, w, xs, ws, ws_size, bias, res, out, static_cast<int>(M), static_cast<int>(N),
-                           static_cast<int>(K), kGroupM);
-    else
-        hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C, false>), dim3(tiles), dim3(C::kThreads), 0, stream,
-                           q, w, xs, ws, ws_size, bias, res, out, static_cast<int>(M), static_cast<int>(N),
-                           static_cast<int>(K), kGroupM);
 }
 
 // Compute units of the current device (cached per device).
@@ -119,7 +33,6 @@ static int device_cus() {
 // 15% fewer bytes per MFMA operation than 256 x 192).  192-token tiles cut
 // M = 11712 exactly; 384 x 192 tiles fill the N = 3072 GEMMs in 2 rounds of
 // 488 tiles (95%), where 256 x 256 makes 552 tiles (3 rounds, 72% full).
-// Returns 0 (256 x 192), 1 (256 x 256) or 2 (384 x 192).
 static int default_tile(int64_t M, int64_t N) {
     const int64_t cus = device_cus();
     auto cost = [&](int64_t bn, int64_t bm, double speed) {
@@ -127,71 +40,64 @@ static int default_tile(int64_t M, int64_t N) {
         return static_cast<double>((tiles + cus - 1) / cus) * static_cast<double>(bn * bm) / speed;
     };
     const double c0 = cost(256, 192, 1.0), c1 = cost(256, 256, 1.06), c2 = cost(384, 192, 1.045);
-    if (c1 < c0 && c1 <= c2) return 1;
-    if (c2 < c0) return 2;
-    return 0;
+    if (c1 < c0 && c1 <= c2) return W8A8_GEMM_TILE_256x256;
+    if (c2 < c0) return W8A8_GEMM_TILE_384x192;
+    return W8A8_GEMM_TILE_256x192;
 }
 
-template <int ODT, int MODE, bool GELU>
-static bool try_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                    int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
-                    int64_t N, int64_t K, hipStream_t stream) {
-    const int choice = mainloop_choice();
-    // whole K tiles only (the DMA ring has no tail masking)
-    if (choice == 0) return false;
-    const int tile = choice == 5 ? default_tile(M, N) : -1;
-    if (tile == 1 && K % CfgN256M256W8::BK == 0) {
-        launch_dma<ODT, MODE, GELU, CfgN256M256W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
-        return true;
+// The main loop w8a8_gemm_dequant runs for a shape (operands 16-byte aligned)
+// and a requested tile (W8A8_GEMM_TILE_* code, AUTO = by shape).  A requested
+// DMA tile that does not take the shape falls back to the automatic choice.
+int gemm_config(int64_t M, int64_t N, int64_t K, int requested) {
+    if (!(K % 16 == 0 && M < (1ll << 31) / 2 && N < (1ll << 31) / 2 && M * K < (1ll << 40)))
+        return W8A8_GEMM_TILE_GENERIC;
+    switch (requested) {
+        case W8A8_GEMM_TILE_256x192: if (dma_fits<CfgN256M192W8>(K)) return requested; break;
+        case W8A8_GEMM_TILE_256x256: if (dma_fits<CfgN256M256W8>(K)) return requested; break;
+        case W8A8_GEMM_TILE_384x192: if (dma_fits<CfgN384M192W8>(K)) return requested; break;
+        case W8A8_GEMM_TILE_256x128: if (dma_fits<CfgN256M128>(K)) return requested; break;
+        case W8A8_GEMM_TILE_REGS: return requested;
+        case W8A8_GEMM_TILE_GENERIC: return requested;
+        default: break;
     }
-    if ((tile == 2 || choice == 7) && K % CfgN384M192W8::BK == 0) {
-        launch_dma<ODT, MODE, GELU, CfgN384M192W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
-        return true;
-    }
-    if ((choice == 5 || choice == 6) && K % CfgN256M192W8::BK == 0) {
-        launch_dma<ODT, MODE, GELU, CfgN256M192W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
-        return true;
-    }
-    if (choice == 4 && K % CfgN256M256W8::BK == 0) {
-        launch_dma<ODT, MODE, GELU, CfgN256M256W8>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
-        return true;
-    }
-    if (choice == 3 && K % CfgN256M256::BK == 0) {
-        launch_dma<ODT, MODE, GELU, CfgN256M256>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
-        return true;
-    }
-    if (K % CfgN256M128::BK != 0) return false;
-    launch_dma<ODT, MODE, GELU, CfgN256M128>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
-    return true;
+    const int tile = default_tile(M, N);
+    if (tile == W8A8_GEMM_TILE_256x256 && dma_fits<CfgN256M256W8>(K)) return tile;
+    if (tile == W8A8_GEMM_TILE_384x192 && dma_fits<CfgN384M192W8>(K)) return tile;
+    if (dma_fits<CfgN256M192W8>(K)) return W8A8_GEMM_TILE_256x192;
+    if (dma_fits<CfgN256M128>(K)) return W8A8_GEMM_TILE_256x128;
+    return W8A8_GEMM_TILE_REGS;
 }
 
-// One output mode of one output dtype: the DMA main loop where it applies, the
-// register-staged main loop for other K % 16 == 0 shapes, else the generic kernel.
-template <int ODT, int MODE, bool GELU>
-static void gemm_dispatch(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
-                          int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
-                          int64_t N, int64_t K, hipStream_t stream) {
-    const bool fast = gemm_mfma_supported(q, 1, w, M, N, K);
-    if (fast && try_dma<ODT, MODE, GELU>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream)) return;
-    if (fast) launch_mfma<ODT, MODE, GELU, -1>(q, nullptr, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);
-    else hipLaunchKernelGGL((gemm_generic<ODT, MODE, GELU>), dim3(static_cast<unsigned>((M * N + 255) / 256)),
-                            dim3(256), 0, stream, q, w, xs, ws, ws_size, bias, res, out, M, N, K);
-}
+#define W8A8_GEMM_EXTERN(ODT, MODE, GELU)                                                          \
+    extern template void gemm_dispatch<ODT, MODE, GELU>(const int8_t*, const int8_t*, const float*, const float*, \
+                                                        int64_t, const void*, const Residual&, void*, int64_t,  \
+                                                        int64_t, int64_t, int, hipStream_t);
+W8A8_GEMM_EXTERN(W8A8_BF16, 0, false)
+W8A8_GEMM_EXTERN(W8A8_BF16, 0, true)
+W8A8_GEMM_EXTERN(W8A8_BF16, 2, false)
+W8A8_GEMM_EXTERN(W8A8_F16, 0, false)
+W8A8_GEMM_EXTERN(W8A8_F16, 0, true)
+W8A8_GEMM_EXTERN(W8A8_F16, 2, false)
+W8A8_GEMM_EXTERN(W8A8_F32, 0, false)
+W8A8_GEMM_EXTERN(W8A8_F32, 0, true)
+W8A8_GEMM_EXTERN(W8A8_F32, 2, false)
+W8A8_GEMM_EXTERN(W8A8_F32, 1, false)
+#undef W8A8_GEMM_EXTERN
 
 // res == nullptr: no residual.  The int32 mode is instantiated once (f32
 // storage type), the residual mode without GELU.
 void launch_gemm(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                  int64_t ws_size, const void* bias, const Residual* res, void* out, int out_dtype,
-                 int64_t M, int64_t N, int64_t K, bool gelu, bool int32_out, hipStream_t stream) {
+                 int64_t M, int64_t N, int64_t K, bool gelu, bool int32_out, int tile, hipStream_t stream) {
     if (int32_out) {
-        gemm_dispatch<W8A8_F32, 1, false>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, stream);
+        gemm_dispatch<W8A8_F32, 1, false>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, tile, stream);
         return;
     }
 #define W8A8_GEMM_CASE(ODT)                                                                       \
     if (out_dtype == ODT) {                                                                       \
-        if (res) gemm_dispatch<ODT, 2, false>(q, w, xs, ws, ws_size, bias, *res, out, M, N, K, stream); \
-        else if (gelu) gemm_dispatch<ODT, 0, true>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, stream); \
-        else gemm_dispatch<ODT, 0, false>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, stream); \
+        if (res) gemm_dispatch<ODT, 2, false>(q, w, xs, ws, ws_size, bias, *res, out, M, N, K, tile, stream); \
+        else if (gelu) gemm_dispatch<ODT, 0, true>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, tile, stream); \
+        else gemm_dispatch<ODT, 0, false>(q, w, xs, ws, ws_size, bias, kNoResidual, out, M, N, K, tile, stream); \
         return;                                                                                   \
     }
     W8A8_GEMM_CASE(W8A8_BF16)

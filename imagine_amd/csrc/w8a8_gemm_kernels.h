@@ -302,7 +302,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mfma(
 // ---------------------------------------------------------------- LDS-DMA main loop
 //
 // Same MFMA tiling and accumulator layout as gemm_mfma, but the K tiles travel
-// from global memory straight into LDS (global_load_lds_dwordx4: each lane
+// from global memory straight into LDS (buffer_load_dwordx4 ... lds: each lane
 // moves 16 bytes, a wave fills 1 KB of contiguous LDS), through a ring of
 // STAGES buffers, so no VGPRs stage the tiles and no LDS write instructions
 // are issued.  The LDS tile is unpadded (BK bytes per row).  Bank conflicts of
@@ -352,7 +352,6 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 }
 
 #define W8A8_LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
-#define W8A8_GLB_PTR(p) ((const __attribute__((address_space(1))) void*)(p))
 
 // Word 3 of a raw buffer resource on gfx9 (32-bit data format, no swizzle).
 // Offsets are checked by the host to stay below 2^31 - the tile bytes.
@@ -497,12 +496,13 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
                 uint2 p;
                 if constexpr (GELU && ODT == W8A8_BF16) {
                     // round the pre-activations in pairs, then GELU in pairs
+                    // (gelu_tanh_fast: within one bf16 ulp, see w8a8_common.h)
                     float v[4];
                     static_for<0, 4>([&](auto e) {
                         v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], false);
                     });
-                    p.x = gelu_bf16x2(pack2_bf16(v[0], v[1]));
-                    p.y = gelu_bf16x2(pack2_bf16(v[2], v[3]));
+                    p.x = gelu_bf16x2_fast(pack2_bf16(v[0], v[1]));
+                    p.y = gelu_bf16x2_fast(pack2_bf16(v[2], v[3]));
                 } else {
                     float v[4];
                     static_for<0, 4>([&](auto e) {
@@ -550,7 +550,7 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
     }
 }
 
-template <int ODT, int MODE, bool GELU, class C, bool BUF>
+template <int ODT, int MODE, bool GELU, class C>
 __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     const int8_t* __restrict__ q, const int8_t* __restrict__ w, const float* __restrict__ xs,
     const float* __restrict__ ws, int64_t ws_size, const void* __restrict__ bias, Residual res,
@@ -597,10 +597,13 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     // Source of each wave-load this lane takes part in: wave-load L (global
     // index j * kWaves + wave, L < kWaveLoads) fills LDS chunks [64 L, 64 L + 64)
     // of the stage; chunk p holds row p / CPR, logical chunk (p % CPR) ^ swz(row).
-    // BUF: byte offsets into a buffer resource per operand (the K offset of a
-    // tile goes in the scalar offset), else 64-bit global addresses.
+    // Byte offsets into a buffer resource per operand (the K offset of a
+    // tile goes in the scalar offset).  Each operand's resource is based at
+    // the block's first tile row, so offsets stay below BN * K (or BM * K)
+    // bytes whatever the operand's size (the host checks that bound).
+    const int8_t* const wb = w + static_cast<int64_t>(n_base) * K;
+    const int8_t* const qb = q + static_cast<int64_t>(m_base) * K;
     uint32_t voff[kLoadsPerThread];
-    const int8_t* src[BUF ? 1 : kLoadsPerThread];
 #pragma unroll
     for (int j = 0; j < kLoadsPerThread; ++j) {
         const int L = j * C::kWaves + wave < C::kWaveLoads ? j * C::kWaves + wave : C::kWaveLoads - 1;
@@ -608,11 +611,10 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
         const int p = (is_w ? L : L - kWWaveLoads) * 64 + lane;
         const int r = p / CPR;
         const int c = (p % CPR) ^ swz<BK>(r);
-        int row = (is_w ? n_base : m_base) + r;
+        const int base = is_w ? n_base : m_base;
         const int lim = is_w ? N : M;
-        row = row < lim ? row : lim - 1;
+        const int row = base + r < lim ? r : lim - 1 - base;   // clamped to the last row, relative
         voff[j] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + c * 16;
-        if constexpr (!BUF) src[j] = (is_w ? w : q) + static_cast<int64_t>(row) * K + c * 16;
     }
     auto issue = [&](int kt, int stage) {
         const int k0 = kt * BK;
@@ -621,12 +623,8 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
             const int L = j * C::kWaves + wave;
             if (C::kWavesWithMore != 0 && L >= C::kWaveLoads) break;   // wave-uniform
             int8_t* dst = lds + stage * kTileBytes + L * 1024;
-            if constexpr (BUF) {
-                buffer_load_lds16(L < kWWaveLoads ? static_cast<const void*>(w) : static_cast<const void*>(q), dst,
-                                  voff[j], k0);
-            } else {
-                __builtin_amdgcn_global_load_lds(W8A8_GLB_PTR(src[j] + k0), W8A8_LDS_PTR(dst), 16, 0, 0);
-            }
+            buffer_load_lds16(L < kWWaveLoads ? static_cast<const void*>(wb) : static_cast<const void*>(qb), dst,
+                              voff[j], k0);
         }
     };
 

@@ -12,7 +12,6 @@
 // exchange for 4-wave rows), and the int8 codes leave as 64-bit stores.
 // Rows that do not fit, or unaligned operands, take the generic kernel.
 #include <algorithm>
-#include <cstdlib>
 
 #include "w8a8_common.h"
 
@@ -54,8 +53,8 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
         return D::load(e[i]);
     };
     // The input activation once per element: raw holds T(gelu_tanh(x)) from
-    // here on (exactly representable in T), so both passes read activated
-    // values without evaluating the activation again.
+    // here on, so both passes read activated values.  16-bit inputs look the
+    // result up (w8a8_gelu_tables.h); fp32 inputs evaluate it.
     if constexpr (GELU) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
@@ -65,11 +64,9 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
 #pragma unroll
                 for (int h = 0; h < 4; ++h) {
                     if constexpr (D::bytes == 4) {
-                        wv[h] = __float_as_uint(gelu_tanh(__uint_as_float(wv[h])));
+                        wv[h] = __float_as_uint(gelu_f32(__uint_as_float(wv[h])));
                     } else {
-                        const float lo = D::load(static_cast<typename D::storage>(wv[h] & 0xffffu));
-                        const float hi = D::load(static_cast<typename D::storage>(wv[h] >> 16));
-                        wv[h] = D::store2(gelu_tanh(lo), gelu_tanh(hi));
+                        wv[h] = gelu_bits<DT>(wv[h] & 0xffffu) | (gelu_bits<DT>(wv[h] >> 16) << 16);
                     }
                 }
             }
@@ -147,7 +144,7 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
     float amax = 0.0f;
     for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
         float f = D::load(x[k]);
-        if constexpr (GELU) f = D::round(gelu_tanh(f));
+        if constexpr (GELU) f = gelu_value<DT>(f);
         amax = fmaxf(amax, fabsf(f));
     }
     amax = wave_max(amax);
@@ -160,7 +157,7 @@ __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict
     const RowQuant rq = row_quant<DT>(s);
     for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
         float f = D::load(x[k]);
-        if constexpr (GELU) f = D::round(gelu_tanh(f));
+        if constexpr (GELU) f = gelu_value<DT>(f);
         q[row * K + k] = static_cast<int8_t>(quant_elem<DT>(f, rq));
     }
 }
@@ -178,15 +175,6 @@ static void launch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t K
 // which keeps more waves streaming per row (K = 3072 bf16, 384 chunks: two
 // waves of 3 chunks per lane, every lane busy, ~23.3 us; four waves of 2,
 // ~24.6 us; one wave of 6, 26.1 us; a plain copy of the same bytes 21.8 us).
-// W8A8_QUANT_ROWS=4 keeps rows of 257..384 chunks on 4 waves (tuning knob).
-static bool quant_two_wave_rows() {
-    static const bool on = [] {
-        const char* e = std::getenv("W8A8_QUANT_ROWS");
-        return !(e && e[0] == '4');
-    }();
-    return on;
-}
-
 template <int DT, bool GELU, bool SO>
 static bool dispatch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, int recip,
                          hipStream_t stream) {
@@ -195,7 +183,7 @@ static bool dispatch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t
     if (nchunks <= 64) launch_vec<DT, 1, 1, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 128) launch_vec<DT, 1, 2, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 256) launch_vec<DT, 4, 1, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
-    else if (nchunks <= 384 && quant_two_wave_rows()) launch_vec<DT, 2, 3, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
+    else if (nchunks <= 384) launch_vec<DT, 2, 3, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 512) launch_vec<DT, 4, 2, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 768) launch_vec<DT, 4, 3, 1, GELU, SO>(x, q, xs, M, K, recip, stream);
     else if (nchunks <= 1024) launch_vec<DT, 4, 4, 1, GELU, SO>(x, q, xs, M, K, recip, stream);

@@ -187,8 +187,20 @@ def gemv_dequant(q, w, xs, ws, bias, out_dtype, gelu=False):
     return out
 
 
-def gemm_dequant(q, w, xs, ws, bias, out_dtype, gelu=False, out=None):
-    """INT8 GEMM + fused dequant epilogue (the reference's ``cutlass_int8_dequant``)."""
+def gemm_config(m, n, k, tile=_lib.TILE_AUTO, gelu=False):
+    """Name of the GEMM main loop ``gemm_dequant`` runs for an m x n x k product
+    (16-byte aligned operands) when ``tile`` is requested: "256x192",
+    "256x256", "384x192", "256x128", "regs" or "generic"."""
+    flags = _lib.GEMM_TILE(tile) | (_lib.ACT_GELU_TANH if gelu else 0)
+    code = _lib.load().w8a8_gemm_config(m, n, k, flags)
+    if code < 0:
+        raise ValueError(f"bad GEMM query {m}x{n}x{k} tile {tile}")
+    return _lib.TILE_NAMES[code]
+
+
+def gemm_dequant(q, w, xs, ws, bias, out_dtype, gelu=False, out=None, tile=_lib.TILE_AUTO):
+    """INT8 GEMM + fused dequant epilogue (the reference's ``cutlass_int8_dequant``).
+    ``tile`` requests a main loop (``_lib.TILE_*``; every one gives the same bits)."""
     _require_cuda(q, w, xs, ws, bias)
     M, K = q.shape
     N = w.shape[0]
@@ -197,11 +209,11 @@ def gemm_dequant(q, w, xs, ws, bias, out_dtype, gelu=False, out=None):
     _lib.check(_lib.load().w8a8_gemm_dequant(
         _ptr(q), _ptr(w), _ptr(xs), _ptr(ws), ws.numel(), _ptr(bias), _ptr(out),
         _dtype_code(out_dtype, "INT8 linear output"), M, N, K,
-        _lib.ACT_GELU_TANH if gelu else 0, _stream(q.device)))
+        (_lib.ACT_GELU_TANH if gelu else 0) | _lib.GEMM_TILE(tile), _stream(q.device)))
     return out
 
 
-def gemm_i32(q, w, out=None):
+def gemm_i32(q, w, out=None, tile=_lib.TILE_AUTO):
     """INT8 GEMM with int32 output (the reference's ``cublas_gemm_int8``)."""
     _require_cuda(q, w)
     M, K = q.shape
@@ -209,8 +221,8 @@ def gemm_i32(q, w, out=None):
     if out is None:
         out = torch.empty((M, N), dtype=torch.int32, device=q.device)
     _lib.check(_lib.load().w8a8_gemm_dequant(
-        _ptr(q), _ptr(w), None, None, 1, None, _ptr(out), _lib.F32, M, N, K, _lib.OUT_INT32,
-        _stream(q.device)))
+        _ptr(q), _ptr(w), None, None, 1, None, _ptr(out), _lib.F32, M, N, K,
+        _lib.OUT_INT32 | _lib.GEMM_TILE(tile), _stream(q.device)))
     return out
 
 
@@ -237,7 +249,8 @@ def _residual_operands(residual, scale, m, n, device, dtype):
     return r, s
 
 
-def gemm_dequant_residual(q, w, xs, ws, bias, out_dtype, residual, residual_scale, out=None):
+def gemm_dequant_residual(q, w, xs, ws, bias, out_dtype, residual, residual_scale, out=None,
+                          tile=_lib.TILE_AUTO):
     """INT8 GEMM + dequant + the pre-norm block's residual in one epilogue (the
     reference's ``cutlass_int8_dequant_residual``)."""
     _require_cuda(q, w, xs, ws, bias)
@@ -248,7 +261,8 @@ def gemm_dequant_residual(q, w, xs, ws, bias, out_dtype, residual, residual_scal
         out = torch.empty((M, N), dtype=out_dtype, device=q.device)
     _lib.check(_lib.load().w8a8_gemm_dequant_residual(
         _ptr(q), _ptr(w), _ptr(xs), _ptr(ws), ws.numel(), _ptr(bias), _ptr(rs), rs.numel(), _ptr(r),
-        _ptr(out), _dtype_code(out_dtype, "INT8 linear output"), M, N, K, 0, _stream(q.device)))
+        _ptr(out), _dtype_code(out_dtype, "INT8 linear output"), M, N, K, _lib.GEMM_TILE(tile),
+        _stream(q.device)))
     return out
 
 

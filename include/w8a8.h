@@ -59,6 +59,24 @@ extern "C" {
 #define W8A8_GIVEN_SCALE (1u << 5)   /* w8a8_quantize_tensorwise: *scale holds the scale
                                         to quantize with (the reference's scale argument) */
 
+/* GEMM main loop (w8a8_gemm_dequant, w8a8_gemm_dequant_residual): flag bits
+ * 8..11 hold a W8A8_GEMM_TILE_* code, W8A8_GEMM_TILE(code).  AUTO (0) lets
+ * the shape choose; any other code requests that main loop, and a DMA tile
+ * that does not take the shape (K not a multiple of its K tile) falls back to
+ * the automatic choice.  Every main loop gives identical results.  No
+ * reference counterpart (CUTLASS picks its tile in its own dispatch,
+ * cutlass_gemm_int8.cu:190-269); used to test and time each main loop. */
+#define W8A8_GEMM_TILE_AUTO 0
+#define W8A8_GEMM_TILE_256x192 1     /* weight rows x tokens per block, 8 waves, 128-byte K tiles */
+#define W8A8_GEMM_TILE_256x256 2     /* 8 waves, 128-byte K tiles */
+#define W8A8_GEMM_TILE_384x192 3     /* 8 waves, 128-byte K tiles */
+#define W8A8_GEMM_TILE_256x128 4     /* 4 waves, two blocks per CU, 64-byte K tiles */
+#define W8A8_GEMM_TILE_REGS 5        /* register-staged main loop, K % 16 == 0 */
+#define W8A8_GEMM_TILE_GENERIC 6     /* one thread per output, any shape and alignment */
+#define W8A8_GEMM_TILE_SHIFT 8
+#define W8A8_GEMM_TILE_MASK (0xFu << W8A8_GEMM_TILE_SHIFT)
+#define W8A8_GEMM_TILE(code) ((uint32_t)(code) << W8A8_GEMM_TILE_SHIFT)
+
 const char* w8a8_last_error(void);
 int w8a8_last_accelerator_code(void);
 /* Library version string ("w8a8-hip <major>.<minor> gfx950"). */
@@ -91,10 +109,17 @@ int w8a8_gemv_dequant(const int8_t* q, const int8_t* w, const float* xs, const f
  * called at cuda_linear.rs:745-763, and, with W8A8_OUT_INT32, `cublas_gemm_int8`
  * (cublas_gemm_int8.cu:176-221, called at cuda_linear.rs:765-779):
  *   out[m,n] = O(fma(float(sum_k q[m,k] w[n,k]) * xs[m], ws[n], bias[n]))
- * Flags: W8A8_ACT_GELU_TANH, W8A8_OUT_INT32 (xs, ws, bias ignored). */
+ * Flags: W8A8_ACT_GELU_TANH, W8A8_OUT_INT32 (xs, ws, bias ignored),
+ * W8A8_GEMM_TILE(code). */
 int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                       int64_t ws_size, const void* bias, void* out, int out_dtype,
                       int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream);
+
+/* The W8A8_GEMM_TILE_* code of the main loop w8a8_gemm_dequant launches for
+ * M x N x K with these flags (its tile bits), for 16-byte aligned operands
+ * (unaligned ones take W8A8_GEMM_TILE_GENERIC), on the current device.  A
+ * query with no reference counterpart: tests use it to know which kernel ran. */
+int w8a8_gemm_config(int64_t M, int64_t N, int64_t K, uint32_t flags);
 
 /* GEMM with the fused residual epilogue of the pre-norm block:
  *   lin[m,n] = O(fma(float(sum_k q[m,k] w[n,k]) * xs[m], ws[n], bias[n]))
@@ -103,7 +128,8 @@ int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const f
  * cutlass_gemm_int8.cu:122-188), called at cuda_linear.rs:724-742; the same
  * single fma as the crate's eager apply_residual on the GPU (int8_linear.rs:99-111).
  * rscale (rscale_size 1 or N entries) and resid ([M, N]) are in the output
- * dtype.  No flags (an output activation or int32 output is rejected). */
+ * dtype.  Flags: W8A8_GEMM_TILE(code) only (an output activation or int32
+ * output is rejected). */
 int w8a8_gemm_dequant_residual(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                                int64_t ws_size, const void* bias, const void* rscale,
                                int64_t rscale_size, const void* resid, void* out, int out_dtype,

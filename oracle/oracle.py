@@ -48,6 +48,8 @@ def lib():
         f.w8o_f32_to_f16_n.argtypes = [p, p, i64]
         f.w8o_gelu_tanh.argtypes = [ctypes.c_float]
         f.w8o_gelu_tanh.restype = ctypes.c_float
+        f.w8o_tanh_cr.argtypes = [ctypes.c_float]
+        f.w8o_tanh_cr.restype = ctypes.c_float
         f.w8o_round_to.argtypes = [ctypes.c_float, i32]
         f.w8o_round_to.restype = ctypes.c_float
     return _lib

@@ -23,7 +23,9 @@
  *                        int8_mm golden vectors (reference_int8_linear.py:18-30).
  *   w8o_epilogue_kitchen reference CUDA payloads (GEMM/GEMV/M1 routes, all dtypes).
  *   w8o_epilogue_eager   reference eager_int8_linear CPU payloads.
- *   w8o_gelu_tanh        reference gelu_tanh activation payloads (1 bf16 ulp).
+ *   w8o_gelu_tanh        reference gelu_tanh activation payloads; every bf16 / fp16
+ *                        value against ATen (equal outside the saturated tail);
+ *                        its tanh against an 80-bit long double evaluation.
  *   w8o_residual         reference CUDA residual payloads (fused, unaligned and
  *                        eager residual modes of the GEMM, GEMV and M=1 routes).
  *   w8o_quant_tensorwise reference tensorwise golden vectors
@@ -124,13 +126,23 @@ float w8o_round_to(float v, int dtype) { return round_to(v, dtype); }
  *   0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3)))
  * Applied by the reference as input_act="gelu_tanh"
  * (inference/src/int8_linear.rs:37-41 -> x.gelu("tanh")).  Computed in fp32 for
- * 16-bit dtypes (ATen's opmath), result rounded to the tensor dtype. */
+ * 16-bit dtypes (ATen's opmath), result rounded to the tensor dtype.
+ *
+ * tanh itself is the correctly rounded fp32 value: the double-precision tanh
+ * of the fp32 argument, rounded once to fp32.  A 1-ulp tanhf (glibc's, ATen's
+ * vectorised one) rounds the same on nearly every argument; where they differ
+ * the reference's own implementations differ from each other too (ATen's
+ * vector tanh saturates to -1 a little early, so four bf16 inputs near -5.1
+ * give -0 there instead of -1.5e-7).  The correctly rounded form is the one
+ * both agree with elsewhere, and it is what this build binds to. */
+float w8o_tanh_cr(float u) { return (float)tanh((double)u); }
+
 float w8o_gelu_tanh(float x) {
     const float kBeta = (float)(1.41421356237309504880 * 1.12837916709551257390 * 0.5);
     const float kKappa = 0.044715f;
     float x_cube = x * x * x;
     float inner = kBeta * (x + kKappa * x_cube);
-    return 0.5f * x * (1.0f + tanhf(inner));
+    return 0.5f * x * (1.0f + w8o_tanh_cr(inner));
 }
 
 /* ------------------------------------------------------------------------ */

@@ -2,9 +2,11 @@
 
 Bar: int8 codes, row scales and int32 accumulators bit-exact; epilogue
 outputs bit-exact against the oracle's single-rounding form (the same formula
-the reference's CUDA routes use); GELU outputs within one output ulp plus an
-absolute 2^-22 (libm tanhf vs the device tanhf).  Also runs the reference's
-own CUDA golden payloads through the operator.
+the reference's CUDA routes use), GELU included (16-bit GELU is a table
+lookup of the correctly rounded form; fp32 GELU evaluates tanh in double),
+except the GELU of the LDS-staged bf16 GEMM epilogue (the fused FFN-up path):
+a formula held to one bf16 ulp with at least 99.9% of outputs bit-equal.
+Also runs the reference's own CUDA golden payloads through the operator.
 """
 import numpy as np
 import pytest
@@ -64,6 +66,16 @@ def make_w(n, k, seed):
     return torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
 
 
+def assert_gelu_close(got, want, dtype="bf16"):
+    """The staged bf16 GELU epilogue's bar: one output ulp (plus 2^-22
+    absolute for the saturated negative tail), at least 99.9% bit-equal."""
+    a = O.to_f32(got, dtype).astype(np.float64)
+    b = O.to_f32(want, dtype).astype(np.float64)
+    bad = np.abs(a - b) > np.abs(b) * 2.0**-7 + 2.0**-22
+    assert not bad.any(), f"{int(bad.sum())} outputs off by more than one ulp"
+    assert (got == want).mean() > 0.999
+
+
 def ulp_close(got, want, dtype, abs_floor=0.0):
     a = O.to_f32(got, dtype).astype(np.float64)
     b = O.to_f32(want, dtype).astype(np.float64)
@@ -103,15 +115,39 @@ def test_quantize_unaligned_input_takes_generic_path():
     assert np.array_equal(s.cpu().numpy().reshape(-1), s_ref)
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
 def test_quantize_gelu_input_act(dtype):
+    """The GELU-tanh input activation (the reference's FFN-down input form):
+    codes and scales bit for bit against the oracle."""
     x = make_x(64, 3072, dtype, seed=4)
     q, s = W.quantize_rowwise(x.to(DEV), input_act="gelu_tanh")
     q_ref, s_ref = O.quant_rowwise(storage(x, dtype), dtype, act=1)
-    qd = q.cpu().numpy().astype(np.int32) - q_ref.astype(np.int32)
-    assert np.abs(qd).max() <= 1 and (qd != 0).mean() < 1e-3
-    sd = np.abs(s.cpu().numpy().reshape(-1) / s_ref - 1)
-    assert sd.max() <= 2.0**-7
+    assert np.array_equal(q.cpu().numpy(), q_ref)
+    assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("aligned", [True, False], ids=["vector", "generic"])
+def test_quantize_gelu_every_16bit_pattern_bit_exact(dtype, aligned):
+    """Every finite 16-bit input through the quantizer's GELU input
+    activation: row i repeats pattern i eight times, so its scale is
+    |T(gelu(x))| / 127 and its codes expose the activated value.  Codes and
+    scales bit for bit against the oracle, on the vector kernel and (an
+    unaligned copy) the generic one."""
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    bits = bits[np.isfinite(O.to_f32(bits, dtype))]
+    rows = np.repeat(bits[:, None], 8, axis=1)
+    xa = from_storage(rows, dtype)
+    if not aligned:
+        buf = torch.empty(rows.size + 8, dtype=TD[dtype], device=DEV)
+        xu = buf[1:1 + rows.size].view(rows.shape)
+        xu.copy_(xa)
+        assert xu.data_ptr() % 16 != 0
+        xa = xu
+    q, s = W.quantize_rowwise(xa, input_act="gelu_tanh")
+    q_ref, s_ref = O.quant_rowwise(rows, dtype, act=1)
+    assert np.array_equal(s.cpu().numpy().reshape(-1).view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(q.cpu().numpy(), q_ref)
 
 
 def test_quantize_gelu_vector_and_generic_kernels_agree_for_every_bf16():
@@ -200,10 +236,10 @@ def test_gemm_dequant_epilogue_bit_exact(odt, with_bias, ws_scalar):
 
 
 @pytest.mark.parametrize("odt", ["bf16", "f16", "f32"])
-def test_gemm_gelu_epilogue_within_one_ulp(odt):
-    """GELU-tanh epilogue: within one output ulp of the oracle (libm tanhf form)
-    plus an absolute 2^-22 for the saturated negative tail; fp32 outputs, which
-    no 16-bit rounding hides, within 2^-18 relative."""
+def test_gemm_gelu_epilogue_bit_exact(odt):
+    """GELU-tanh epilogue against the oracle: bit for bit for fp16 and fp32
+    (fp32's tanh is the double-precision tanh rounded once); bf16 takes the
+    staged epilogue here (one ulp)."""
     m, n, k = 260, 384, 768
     x = make_x(m, k, "bf16", seed=8)
     q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
@@ -214,16 +250,11 @@ def test_gemm_gelu_epilogue_within_one_ulp(odt):
                          ws.to(DEV), bias.to(DEV), TD[odt], gelu=True)
     want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt),
                               odt, act=1)
-    got = storage(out, odt)
-    a = O.to_f32(got, odt).astype(np.float64)
-    b = O.to_f32(want, odt).astype(np.float64)
-    rel = {"bf16": 2.0**-7, "f16": 2.0**-10, "f32": 2.0**-18}[odt]
-    bad = np.abs(a - b) > np.abs(b) * rel + 2.0**-22
-    if bad.any():
-        i = np.argmax(np.abs(a - b) - np.abs(b) * rel)
-        pytest.fail(f"{int(bad.sum())} outputs off; worst got {a.flat[i]!r} want {b.flat[i]!r}")
-    if odt != "f32":
-        assert (got == want).mean() > 0.999
+    if odt == "bf16":
+        assert W.gemm_config(m, n, k, gelu=True) in ("256x192", "256x256", "384x192")
+        assert_gelu_close(storage(out, odt), want)
+    else:
+        assert np.array_equal(storage(out, odt), want)
 
 
 def test_gemm_full_size_sampled_rows_bit_exact():
@@ -252,7 +283,8 @@ def test_gemm_full_size_sampled_rows_bit_exact():
 def test_gemm_n3072_tiles_sampled_rows(mode):
     """M = 11712, N = 3072 (the out-proj / FFN-down width, where the default
     tile choice takes 384 x 192 tiles), K = 512: every epilogue mode on 64
-    sampled rows against the oracle (GELU within one ulp, the rest bit-exact)."""
+    sampled rows against the oracle, bit for bit (the staged bf16 GELU to one
+    ulp)."""
     m, k, n = 11712, 512, 3072
     odt = {"bf16_gelu": "bf16", "bf16_residual": "bf16", "int32": "f32"}.get(mode, mode)
     x = make_x(m, k, "bf16", seed=61)
@@ -282,7 +314,7 @@ def test_gemm_n3072_tiles_sampled_rows(mode):
     want = O.epilogue_kitchen(acc_ref, xs_ref, ws.numpy(), storage(bias, odt), odt,
                               act=1 if mode == "bf16_gelu" else 0)
     if mode == "bf16_gelu":
-        _gelu_close(storage(out, odt)[rows], want, odt)
+        assert_gelu_close(storage(out, odt)[rows], want)
     else:
         assert np.array_equal(storage(out, odt)[rows], want)
 
@@ -355,25 +387,18 @@ def test_dequantize_linear_bit_exact():
     assert np.array_equal(storage(out, "f16"), want)
 
 
-def _gelu_close(got, want, odt):
-    """The GELU epilogue's bar: one output ulp plus an absolute 2^-22, and at
-    least 99.9% of 16-bit outputs bit-equal to the oracle's."""
-    a = O.to_f32(got, odt).astype(np.float64)
-    b = O.to_f32(want, odt).astype(np.float64)
-    rel = {"bf16": 2.0**-7, "f16": 2.0**-10, "f32": 2.0**-18}[odt]
-    bad = np.abs(a - b) > np.abs(b) * rel + 2.0**-22
-    assert not bad.any(), f"{int(bad.sum())} outputs off by more than one ulp"
-    if odt != "f32":
-        assert (got == want).mean() > 0.999
-
-
+@pytest.mark.parametrize("tile", [W._lib.TILE_AUTO, W._lib.TILE_256x128, W._lib.TILE_REGS, W._lib.TILE_GENERIC],
+                         ids=lambda t: W._lib.TILE_NAMES[t])
 @pytest.mark.parametrize("odt", ["bf16", "f16"])
-def test_gemm_gelu_epilogue_every_preactivation(odt):
+def test_gemm_gelu_epilogue_every_preactivation(odt, tile):
     """Every finite 16-bit pre-activation through the GEMM's GELU epilogue.
     Zero codes make the accumulators 0, so the pre-activation of channel n is
     fma(0 * xs, ws, bias[n]) = bias[n] exactly; the bias takes every finite bit
     pattern of the output dtype (the saturated tails, the cancelling negative
-    tail, subnormals and signed zeros included)."""
+    tail, subnormals and signed zeros included).  Bit for bit against the
+    oracle on the register-staged and generic main loops and for fp16
+    outputs; the staged bf16 epilogue of the DMA main loops (auto, 256x128)
+    to one ulp."""
     bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
     bits = bits[np.isfinite(O.to_f32(bits, odt))]
     n = (len(bits) + 255) // 256 * 256
@@ -384,13 +409,16 @@ def test_gemm_gelu_epilogue_every_preactivation(odt):
     xs = torch.full((m,), 0.75)
     ws = torch.full((n,), 1.25)
     out = W.gemm_dequant(q.to(DEV), w.to(DEV), xs.to(DEV), ws.to(DEV), from_storage(bias, odt),
-                         TD[odt], gelu=True)
+                         TD[odt], gelu=True, tile=tile)
     want = O.epilogue_kitchen(np.zeros((m, n), np.int32), xs.numpy(), ws.numpy(), bias, odt, act=1)
-    _gelu_close(storage(out, odt), want, odt)
+    if odt == "bf16" and tile in (W._lib.TILE_AUTO, W._lib.TILE_256x128):
+        assert_gelu_close(storage(out, odt), want)
+    else:
+        assert np.array_equal(storage(out, odt), want)
 
 
 @pytest.mark.parametrize("odt", ["bf16", "f16"])
-def test_gemv_gelu_epilogue_within_one_ulp(odt):
+def test_gemv_gelu_epilogue_bit_exact(odt):
     m, n, k = 2, 4096, 3072
     x = make_x(m, k, "bf16", seed=21)
     q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
@@ -401,10 +429,10 @@ def test_gemv_gelu_epilogue_within_one_ulp(odt):
                          ws.to(DEV), bias.to(DEV), TD[odt], gelu=True)
     want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt),
                               odt, act=1)
-    _gelu_close(storage(out, odt), want, odt)
+    assert np.array_equal(storage(out, odt), want)
 
 
-def test_dequantize_linear_gelu_within_one_ulp():
+def test_dequantize_linear_gelu_bit_exact():
     """Dequant + GELU over a wide range of pre-activations, the saturated
     negative tail included (values down to about -12)."""
     m, n = 64, 512
@@ -415,7 +443,7 @@ def test_dequantize_linear_gelu_within_one_ulp():
     bias = (torch.randn(n, generator=g) * 0.5).to(torch.bfloat16)
     out = W.dequantize_linear(acc.to(DEV), xs.to(DEV), ws.to(DEV), bias.to(DEV), torch.bfloat16, gelu=True)
     want = O.epilogue_kitchen(acc.numpy(), xs.numpy(), ws.numpy(), storage(bias, "bf16"), "bf16", act=1)
-    _gelu_close(storage(out, "bf16"), want, "bf16")
+    assert np.array_equal(storage(out, "bf16"), want)
 
 
 def _residual_inputs(m, n, odt, seed):
