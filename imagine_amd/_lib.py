@@ -40,6 +40,8 @@ SIGNATURES = {
     "w8a8_dequantize_linear": (_i, [_p, _p, _p, _i64, _p, _p, _i, _i64, _i64, _u32, _p]),
     "w8a8_int8_linear_workspace_bytes": (_i64, [_i64, _i64]),
     "w8a8_int8_linear": (_i, [_p, _i, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _u32, _p, _i64, _p]),
+    "w8a8_int8_linear_noalloc_max_bytes": (_i64, []),
+    "w8a8_int8_linear_noalloc": (_i, [_p, _i, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _u32, _p]),
     "w8a8_gemm_dequant_residual": (_i, [_p, _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64,
                                         _u32, _p]),
     "w8a8_gemv_dequant_residual": (_i, [_p, _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64,

@@ -21,7 +21,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libw8a8_hip.so"
 SOURCES = ["w8a8_gemm_f32.hip", "w8a8_gemm_bf16.hip", "w8a8_gemm_f16.hip", "w8a8_gemm.hip", "w8a8_quant.hip",
-           "w8a8_glue.hip", "w8a8_convrot.hip", "w8a8_gemv.hip", "w8a8_api.hip"]
+           "w8a8_glue.hip", "w8a8_convrot.hip", "w8a8_gemv.hip", "w8a8_api.hip", "w8a8_noalloc.hip"]
 ARCH = os.environ.get("W8A8_OFFLOAD_ARCH", "gfx950")
 
 

@@ -62,6 +62,19 @@ int fail(int code, const std::string& msg) {
     return code;
 }
 
+}  // namespace
+
+namespace w8a8 {
+// The calling thread's error state, for the entry points of other translation units.
+int set_error(int code, const std::string& msg) { return fail(code, msg); }
+int set_accelerator_error(int hip_code, const std::string& msg) {
+    g_last_accel = hip_code;
+    return fail(W8A8_ERR_ACCELERATOR, msg);
+}
+}  // namespace w8a8
+
+namespace {
+
 int check_launch(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {

@@ -178,6 +178,22 @@ int w8a8_int8_linear(const void* x, int x_dtype, const int8_t* w, const float* w
                      int64_t M, int64_t N, int64_t K, uint32_t flags, void* workspace,
                      int64_t workspace_bytes, hipStream_t stream);
 
+/* w8a8_int8_linear without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * No counterpart in the reference (the crate allocates q and xs per call,
+ * cuda_linear.rs:603-604).  The codes and row scales go to a fixed device
+ * array of W8A8_NOALLOC_SCRATCH_BYTES, one per device, held from this entry's
+ * first call on the device until the process ends; nothing is allocated or
+ * freed per call.  Inputs whose w8a8_int8_linear_workspace_bytes(M, K)
+ * exceeds it fail with W8A8_ERR_VALUE.  Calls on one device share the array:
+ * calls that overlap in time (other streams, other threads) race.  Same
+ * routes, flags and results as w8a8_int8_linear. */
+#define W8A8_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int64_t w8a8_int8_linear_noalloc_max_bytes(void);
+int w8a8_int8_linear_noalloc(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
+                             const void* bias, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                             uint32_t flags, hipStream_t stream);
+
 /* w8a8_int8_linear with the residual of the pre-norm block (the crate's
  * residual / residual_scale kwargs, cuda_linear.rs:700-744 and the eager
  * fallback int8_linear.rs:99-111), fused into the GEMM or GEMV epilogue:

@@ -35,6 +35,14 @@ def test_version_and_workspace_size():
     assert lib.w8a8_int8_linear_workspace_bytes(-1, 5) == -1
 
 
+def test_noalloc_entry_rejects_inputs_beyond_its_scratch_before_touching_memory():
+    lib = _lib.load()
+    assert lib.w8a8_int8_linear_noalloc_max_bytes() == 64 << 20
+    rc = lib.w8a8_int8_linear_noalloc(None, 2, None, None, 1, None, None, 2, 16384, 64, 4096, 0, None)
+    assert rc == _lib.ERR_VALUE
+    assert "fixed scratch of 67108864 bytes" in lib.w8a8_last_error().decode()
+
+
 def _err(rc):
     return rc, _lib.load().w8a8_last_error().decode()
 
