@@ -40,6 +40,40 @@ def flags():
     ]
 
 
+BRIDGE = PKG / "libimagine_kitchen.so"
+
+
+def torch_dir():
+    """LibTorch of this image (headers and libraries), located without importing torch."""
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        raise RuntimeError("the kitchen bridge needs LibTorch headers (the torch package)")
+    return Path(list(spec.submodule_search_locations)[0])
+
+
+def build_bridge(verbose=False):
+    """libimagine_kitchen.so: the reference bridge's imagine_kitchen_call for the
+    W8A8 names, over libw8a8_hip.so (g++, LibTorch headers for at::Tensor)."""
+    t = torch_dir()
+    rocm = Path(hipcc()).resolve().parents[1]
+    with tempfile.TemporaryDirectory(prefix="w8a8_bridge_") as tmp:
+        out = Path(tmp) / BRIDGE.name
+        cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
+               f"-I{t / 'include'}", f"-I{t / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+               f"-I{rocm / 'include'}", f"-I{ROOT / 'include'}", str(CSRC / "kitchen_bridge.cpp"), "-o", str(out),
+               f"-L{PKG}", "-lw8a8_hip", f"-L{t / 'lib'}", "-lc10", "-ltorch_cpu", f"-L{rocm / 'lib'}",
+               "-lamdhip64", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{t / 'lib'}", f"-Wl,-rpath,{rocm / 'lib'}"]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"kitchen bridge build failed:\n{r.stderr[-4000:]}")
+        if verbose and r.stderr.strip():
+            print(r.stderr, file=sys.stderr)
+        shutil.copy2(out, BRIDGE.with_suffix(".so.tmp"))
+        os.replace(BRIDGE.with_suffix(".so.tmp"), BRIDGE)
+    return BRIDGE
+
+
 def build(verbose=False, extra=()):
     cc = hipcc()
     with tempfile.TemporaryDirectory(prefix="w8a8_build_") as tmp:
@@ -74,3 +108,4 @@ def build(verbose=False, extra=()):
 
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_bridge(verbose="-v" in sys.argv))

@@ -95,67 +95,19 @@ template <> struct DType<W8A8_BF16> {
 
 // gelu_tanh(x) = 0.5 * x * (1 + tanh(u)),  u = sqrt(2/pi) * (x + 0.044715 * x^3),
 // the reference's input_act "gelu_tanh" (inference/src/int8_linear.rs:37-41):
-// ATen's operation order in fp32, tanh correctly rounded to fp32.
-//
-// A 16-bit input has 65536 values, so 16-bit GELU is a lookup: the tables of
-// w8a8_gelu_tables.h (generated at build time by imagine_amd/gelu_tables.py,
-// which checks its closed forms on every pattern) hold the rounded result for
-// the inputs where it is not one of the closed forms below.  Exact by
-// construction; every pattern is compared with the oracle on the GPU.
+// ATen's operation order in fp32, tanh correctly rounded to fp32, the result
+// rounded to the tensor's dtype.  Three forms, each exact for its dtype:
+//   bf16  gelu_tanh_fast below, then RNE to bf16.  A bf16 input has 65536
+//         values; for every finite one the result equals the correctly
+//         rounded form (GPU tests run all of them through the quantizer and
+//         through each GEMM main loop's epilogue against the oracle).
+//   fp16  a lookup in kGeluF16Table (w8a8_gelu_tables.h, generated at build
+//         time by imagine_amd/gelu_tables.py): the formula misses 5 of the
+//         63488 finite fp16 inputs.
+//   fp32  evaluated with the double-precision tanh of the fp32 argument,
+//         rounded once (the correctly rounded fp32 tanh in all but vanishingly
+//         rare cases).
 
-// bf16 pattern b (low 16 bits) -> bf16 pattern of gelu_tanh(b).  tab has the
-// kGeluBf16Table layout and may be that global table or an LDS copy.  Written
-// without branches: the table is read at a clamped (always valid) index and
-// the closed forms are selected afterwards, so a run of lookups issues its
-// reads back to back instead of waiting on each one.
-__device__ __forceinline__ uint32_t gelu_bf16_bits(uint32_t b, const uint16_t* tab) {
-    const uint32_t a = b & 0x7fffu;
-    const uint32_t ac = a < kGeluBf16Lo ? kGeluBf16Lo : (a >= kGeluBf16Hi ? kGeluBf16Hi - 1 : a);
-    const uint32_t looked = tab[(b >> 15) * kGeluBf16Span + (ac - kGeluBf16Lo)];
-    const uint32_t half = f32_to_bf16(0.5f * bf16_to_f32(static_cast<uint16_t>(b)));  // 1 + tanh(u) rounds away
-    const uint32_t neg_big = a == 0x7f80u ? 0xffc0u : 0x8000u;     // -inf: 0 * -inf; finite: -0
-    uint32_t big = (b & 0x8000u) ? neg_big : b;                     // tanh(u) = 1: x
-    big = a > 0x7f80u ? (b | 0x40u) : big;                          // NaN: the input, quieted
-    return a < kGeluBf16Lo ? half : (a >= kGeluBf16Hi ? big : looked);
-}
-
-// fp16 pattern b -> fp16 pattern of gelu_tanh(b); the table covers |x| < 6.
-__device__ __forceinline__ uint32_t gelu_f16_bits(uint32_t b, const uint16_t* tab) {
-    const uint32_t a = b & 0x7fffu;
-    if (a >= kGeluF16Hi) {
-        if (a > 0x7c00u) return b | 0x200u;
-        if (b & 0x8000u) return a == 0x7c00u ? 0xfe00u : 0x8000u;
-        return b;
-    }
-    return tab[(b >> 15) * kGeluF16Span + a];
-}
-
-// fp32 input: evaluated, with tanh from the double-precision tanh of the fp32
-// argument rounded once (the correctly rounded fp32 tanh in all but
-// vanishingly rare cases).
-__device__ __forceinline__ float gelu_f32(float x) {
-    const float kBeta = 0.79788456080286535588f;  // sqrt(2) * (2/sqrt(pi)) * 0.5
-    const float kKappa = 0.044715f;
-    const float x_cube = x * x * x;
-    const float inner = kBeta * (x + kKappa * x_cube);
-    const float t = static_cast<float>(tanh(static_cast<double>(inner)));
-    return 0.5f * x * (1.0f + t);
-}
-
-// GELU of the 16-bit pattern b of dtype DT (global tables).
-template <int DT>
-__device__ __forceinline__ uint32_t gelu_bits(uint32_t b) {
-    static_assert(DT != W8A8_F32, "16-bit dtypes only");
-    if constexpr (DT == W8A8_BF16) return gelu_bf16_bits(b, kGeluBf16Table);
-    else return gelu_f16_bits(b, kGeluF16Table);
-}
-
-// The fused GEMM epilogue's GELU (the LDS-staged bf16 path of FFN-up): an
-// evaluation in fewer operations than a lookup, within one bf16 ulp of the
-// exact result and equal to it on all but about 0.1% of inputs.  A branchless
-// LDS copy of the bf16 table measured 12% slower on the whole FFN-up GEMM
-// (11712 x 3072 x 12288: 498 vs 442 us), the global table 18%: the epilogue
-// runs while the matrix cores idle, so its instruction count is what counts.
 // Structure 0.5 x (1 + tanh(u)) as the reference's:
 //   e = x (a + b x^2) = 2u / ln 2           (sqrt(2/pi) and 0.044715 pre-scaled
 //                                            by 2 / ln 2, so exp2 takes -|e|
@@ -168,7 +120,10 @@ __device__ __forceinline__ uint32_t gelu_bits(uint32_t b) {
 //   gelu = (x/2) (1 + copysign(r, x))       (the reference's two roundings:
 //                                            a single fma would turn the -0 of
 //                                            the saturated negative tail into +0)
-// exp2 and the reciprocal are the hardware approximations (about 1 ulp).
+// exp2 and the reciprocal are the hardware approximations (about 1 ulp); the
+// fp32 result carries a few ulps of error, which bf16 rounding never shows.
+// About 14 VALU slots; it runs in the FFN-up epilogue while the matrix cores
+// idle, where a table lookup measured 12-18% slower on the whole GEMM.
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
     const float kA = 2.302208198144325f;      // sqrt(2/pi) * 2 / ln 2
     const float kB = 0.1029432395800235f;     // sqrt(2/pi) * 0.044715 * 2 / ln 2
@@ -179,10 +134,44 @@ __device__ __forceinline__ float gelu_tanh_fast(float x) {
     return (0.5f * x) * (1.0f + __builtin_copysignf(r, x));
 }
 
-// Two bf16 pre-activations packed in one word (low half first) -> their
-// gelu_tanh_fast, rounded and packed the same way (one v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t gelu_bf16x2_fast(uint32_t p) {
+// Two bf16 values packed in one word (low half first) -> their GELU, rounded
+// and packed the same way (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t gelu_bf16x2(uint32_t p) {
     return pack2_bf16(gelu_tanh_fast(__uint_as_float(p << 16)), gelu_tanh_fast(__uint_as_float(p & 0xffff0000u)));
+}
+
+// fp16 pattern b (low 16 bits) -> fp16 pattern of gelu_tanh(b); the table
+// covers |x| < 6, beyond which the result is x (x > 0) or -0 (finite x < 0).
+__device__ __forceinline__ uint32_t gelu_f16_bits(uint32_t b) {
+    const uint32_t a = b & 0x7fffu;
+    const uint32_t looked = kGeluF16Table[(b >> 15) * kGeluF16Span + (a < kGeluF16Hi ? a : kGeluF16Hi - 1)];
+    uint32_t big = (b & 0x8000u) ? (a == 0x7c00u ? 0xfe00u : 0x8000u) : b;   // -inf: 0 * -inf
+    big = a > 0x7c00u ? (b | 0x200u) : big;                                 // NaN: the input, quieted
+    return a < kGeluF16Hi ? looked : big;
+}
+
+__device__ __forceinline__ float gelu_f32(float x) {
+    const float kBeta = 0.79788456080286535588f;  // sqrt(2) * (2/sqrt(pi)) * 0.5
+    const float kKappa = 0.044715f;
+    const float x_cube = x * x * x;
+    const float inner = kBeta * (x + kKappa * x_cube);
+    const float t = static_cast<float>(tanh(static_cast<double>(inner)));
+    return 0.5f * x * (1.0f + t);
+}
+
+// GELU of the 16-bit pattern b of dtype DT.
+template <int DT>
+__device__ __forceinline__ uint32_t gelu_bits(uint32_t b) {
+    static_assert(DT != W8A8_F32, "16-bit dtypes only");
+    if constexpr (DT == W8A8_BF16) return f32_to_bf16(gelu_tanh_fast(bf16_to_f32(static_cast<uint16_t>(b))));
+    else return gelu_f16_bits(b);
+}
+
+// Two 16-bit patterns of dtype DT packed in one word -> their GELU, packed.
+template <int DT>
+__device__ __forceinline__ uint32_t gelu_x2(uint32_t p) {
+    if constexpr (DT == W8A8_BF16) return gelu_bf16x2(p);
+    else return gelu_f16_bits(p & 0xffffu) | (gelu_f16_bits(p >> 16) << 16);
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used

@@ -496,13 +496,12 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
                 uint2 p;
                 if constexpr (GELU && ODT == W8A8_BF16) {
                     // round the pre-activations in pairs, then GELU in pairs
-                    // (gelu_tanh_fast: within one bf16 ulp, see w8a8_common.h)
                     float v[4];
                     static_for<0, 4>([&](auto e) {
                         v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], false);
                     });
-                    p.x = gelu_bf16x2_fast(pack2_bf16(v[0], v[1]));
-                    p.y = gelu_bf16x2_fast(pack2_bf16(v[2], v[3]));
+                    p.x = gelu_bf16x2(pack2_bf16(v[0], v[1]));
+                    p.y = gelu_bf16x2(pack2_bf16(v[2], v[3]));
                 } else {
                     float v[4];
                     static_for<0, 4>([&](auto e) {

@@ -53,8 +53,8 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
         return D::load(e[i]);
     };
     // The input activation once per element: raw holds T(gelu_tanh(x)) from
-    // here on, so both passes read activated values.  16-bit inputs look the
-    // result up (w8a8_gelu_tables.h); fp32 inputs evaluate it.
+    // here on, so both passes read activated values (exact for each dtype,
+    // see gelu_bits in w8a8_common.h).
     if constexpr (GELU) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
@@ -66,7 +66,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
                     if constexpr (D::bytes == 4) {
                         wv[h] = __float_as_uint(gelu_f32(__uint_as_float(wv[h])));
                     } else {
-                        wv[h] = gelu_bits<DT>(wv[h] & 0xffffu) | (gelu_bits<DT>(wv[h] >> 16) << 16);
+                        wv[h] = gelu_x2<DT>(wv[h]);
                     }
                 }
             }

@@ -43,6 +43,26 @@ def test_noalloc_entry_rejects_inputs_beyond_its_scratch_before_touching_memory(
     assert "fixed scratch of 67108864 bytes" in lib.w8a8_last_error().decode()
 
 
+def test_kitchen_bridge_exports_the_bridge_symbols_and_rejects_unknown_names():
+    """libimagine_kitchen.so loads like the crate loads its bridge and answers
+    an unknown name with the bridge's code and text (no device touched)."""
+    bridge = ctypes.CDLL(str(_lib.LIB_PATH.parent / "libimagine_kitchen.so"), mode=ctypes.RTLD_LOCAL)
+    text = re.sub(r"/\*.*?\*/", "", (HEADER.parent / "imagine_kitchen.h").read_text(), flags=re.S)
+    declared = sorted(set(re.findall(r"\b(imagine_[a-z_]+)\s*\(", text)))
+    assert declared == ["imagine_kitchen_call", "imagine_last_accelerator_code", "imagine_last_error",
+                        "imagine_last_metadata"]
+    for name in declared:
+        assert hasattr(bridge, name), name
+    bridge.imagine_kitchen_call.argtypes = [ctypes.c_char_p, ctypes.c_void_p, ctypes.c_size_t,
+                                            ctypes.POINTER(ctypes.c_int64)]
+    bridge.imagine_last_error.restype = ctypes.c_char_p
+    out = ctypes.c_int64(0)
+    assert bridge.imagine_kitchen_call(b"no_such_kernel", None, 0, ctypes.byref(out)) == -1
+    assert bridge.imagine_last_error() == b"Unknown Kitchen kernel"
+    assert bridge.imagine_kitchen_call(b"cutlass_int8_dequant", None, 0, ctypes.byref(out)) == -1
+    assert bridge.imagine_last_error() == b"Kernel argument count mismatch"
+
+
 def _err(rc):
     return rc, _lib.load().w8a8_last_error().decode()
 

@@ -2,10 +2,8 @@
 
 Bar: int8 codes, row scales and int32 accumulators bit-exact; epilogue
 outputs bit-exact against the oracle's single-rounding form (the same formula
-the reference's CUDA routes use), GELU included (16-bit GELU is a table
-lookup of the correctly rounded form; fp32 GELU evaluates tanh in double),
-except the GELU of the LDS-staged bf16 GEMM epilogue (the fused FFN-up path):
-a formula held to one bf16 ulp with at least 99.9% of outputs bit-equal.
+the reference's CUDA routes use), GELU included (GELU-tanh with a correctly
+rounded tanh: every finite bf16 and fp16 input is checked exhaustively).
 Also runs the reference's own CUDA golden payloads through the operator.
 """
 import numpy as np
@@ -64,16 +62,6 @@ def make_x(m, k, dtype, seed, dist="normal"):
 def make_w(n, k, seed):
     g = torch.Generator().manual_seed(seed)
     return torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
-
-
-def assert_gelu_close(got, want, dtype="bf16"):
-    """The staged bf16 GELU epilogue's bar: one output ulp (plus 2^-22
-    absolute for the saturated negative tail), at least 99.9% bit-equal."""
-    a = O.to_f32(got, dtype).astype(np.float64)
-    b = O.to_f32(want, dtype).astype(np.float64)
-    bad = np.abs(a - b) > np.abs(b) * 2.0**-7 + 2.0**-22
-    assert not bad.any(), f"{int(bad.sum())} outputs off by more than one ulp"
-    assert (got == want).mean() > 0.999
 
 
 def ulp_close(got, want, dtype, abs_floor=0.0):
@@ -237,9 +225,8 @@ def test_gemm_dequant_epilogue_bit_exact(odt, with_bias, ws_scalar):
 
 @pytest.mark.parametrize("odt", ["bf16", "f16", "f32"])
 def test_gemm_gelu_epilogue_bit_exact(odt):
-    """GELU-tanh epilogue against the oracle: bit for bit for fp16 and fp32
-    (fp32's tanh is the double-precision tanh rounded once); bf16 takes the
-    staged epilogue here (one ulp)."""
+    """GELU-tanh epilogue, bit for bit against the oracle (fp32 outputs too:
+    their tanh is the double-precision tanh rounded once)."""
     m, n, k = 260, 384, 768
     x = make_x(m, k, "bf16", seed=8)
     q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
@@ -250,11 +237,7 @@ def test_gemm_gelu_epilogue_bit_exact(odt):
                          ws.to(DEV), bias.to(DEV), TD[odt], gelu=True)
     want = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt),
                               odt, act=1)
-    if odt == "bf16":
-        assert W.gemm_config(m, n, k, gelu=True) in ("256x192", "256x256", "384x192")
-        assert_gelu_close(storage(out, odt), want)
-    else:
-        assert np.array_equal(storage(out, odt), want)
+    assert np.array_equal(storage(out, odt), want)
 
 
 def test_gemm_full_size_sampled_rows_bit_exact():
@@ -283,8 +266,7 @@ def test_gemm_full_size_sampled_rows_bit_exact():
 def test_gemm_n3072_tiles_sampled_rows(mode):
     """M = 11712, N = 3072 (the out-proj / FFN-down width, where the default
     tile choice takes 384 x 192 tiles), K = 512: every epilogue mode on 64
-    sampled rows against the oracle, bit for bit (the staged bf16 GELU to one
-    ulp)."""
+    sampled rows against the oracle, bit for bit."""
     m, k, n = 11712, 512, 3072
     odt = {"bf16_gelu": "bf16", "bf16_residual": "bf16", "int32": "f32"}.get(mode, mode)
     x = make_x(m, k, "bf16", seed=61)
@@ -313,10 +295,7 @@ def test_gemm_n3072_tiles_sampled_rows(mode):
     out = W.gemm_dequant(q, wd, xs, ws.to(DEV), bias.to(DEV), TD[odt], gelu=mode == "bf16_gelu")
     want = O.epilogue_kitchen(acc_ref, xs_ref, ws.numpy(), storage(bias, odt), odt,
                               act=1 if mode == "bf16_gelu" else 0)
-    if mode == "bf16_gelu":
-        assert_gelu_close(storage(out, odt)[rows], want)
-    else:
-        assert np.array_equal(storage(out, odt)[rows], want)
+    assert np.array_equal(storage(out, odt)[rows], want)
 
 
 # ---------------------------------------------------------------- GEMV
@@ -396,9 +375,9 @@ def test_gemm_gelu_epilogue_every_preactivation(odt, tile):
     fma(0 * xs, ws, bias[n]) = bias[n] exactly; the bias takes every finite bit
     pattern of the output dtype (the saturated tails, the cancelling negative
     tail, subnormals and signed zeros included).  Bit for bit against the
-    oracle on the register-staged and generic main loops and for fp16
-    outputs; the staged bf16 epilogue of the DMA main loops (auto, 256x128)
-    to one ulp."""
+    oracle, on the staged epilogue of a DMA main loop with one block per CU
+    (auto), of the two-blocks-per-CU one (256x128), and on the register-staged
+    and generic main loops."""
     bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
     bits = bits[np.isfinite(O.to_f32(bits, odt))]
     n = (len(bits) + 255) // 256 * 256
@@ -411,10 +390,7 @@ def test_gemm_gelu_epilogue_every_preactivation(odt, tile):
     out = W.gemm_dequant(q.to(DEV), w.to(DEV), xs.to(DEV), ws.to(DEV), from_storage(bias, odt),
                          TD[odt], gelu=True, tile=tile)
     want = O.epilogue_kitchen(np.zeros((m, n), np.int32), xs.numpy(), ws.numpy(), bias, odt, act=1)
-    if odt == "bf16" and tile in (W._lib.TILE_AUTO, W._lib.TILE_256x128):
-        assert_gelu_close(storage(out, odt), want)
-    else:
-        assert np.array_equal(storage(out, odt), want)
+    assert np.array_equal(storage(out, odt), want)
 
 
 @pytest.mark.parametrize("odt", ["bf16", "f16"])
