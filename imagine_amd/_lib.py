@@ -16,6 +16,8 @@ OUT_INT32 = 1 << 2
 FUSED_QUANT = 1 << 3
 ROUTE_GEMM = 1 << 4
 GIVEN_SCALE = 1 << 5
+# input activation codes
+ACT_CODES = {None: 0, "gelu_tanh": 1, "swiglu": 2, "rms_norm": 3, "situ": 4}
 # GEMM main loops (flag bits 8..11: GEMM_TILE(code))
 TILE_AUTO, TILE_256x192, TILE_256x256, TILE_384x192, TILE_256x128, TILE_REGS, TILE_GENERIC = range(7)
 TILE_NAMES = {TILE_AUTO: "auto", TILE_256x192: "256x192", TILE_256x256: "256x256", TILE_384x192: "384x192",
@@ -33,6 +35,10 @@ SIGNATURES = {
     "w8a8_version": (ctypes.c_char_p, []),
     "w8a8_quantize_rowwise": (_i, [_p, _i, _p, _p, _i64, _i64, _u32, _p]),
     "w8a8_row_scales": (_i, [_p, _i, _p, _i64, _i64, _u32, _p]),
+    "w8a8_input_act": (_i, [_p, _i, _i, _p, ctypes.c_double, _p, _i64, _i64, _p]),
+    "w8a8_quantize_rowwise_act": (_i, [_p, _i, _i, _p, ctypes.c_double, _p, _p, _i64, _i64, _i64, _u32, _p, _i64, _p]),
+    "w8a8_int8_linear_act": (_i, [_p, _i, _i, _p, ctypes.c_double, _p, _p, _i64, _p, _p, _i64, _p, _p, _i, _i64, _i64,
+                                  _i64, _i64, _u32, _p, _i64, _p]),
     "w8a8_gemv_dequant": (_i, [_p, _p, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _u32, _p]),
     "w8a8_gemm_dequant": (_i, [_p, _p, _p, _p, _i64, _p, _p, _i, _i64, _i64, _i64, _u32, _p]),
     "w8a8_gemm_config": (_i, [_i64, _i64, _i64, _u32]),

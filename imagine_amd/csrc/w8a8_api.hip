@@ -29,6 +29,10 @@ void launch_dequant(const int32_t* acc, const float* xs, const float* ws, int64_
                     const void* bias, void* out, int out_dtype, int64_t M, int64_t N, bool gelu,
                     hipStream_t stream);
 bool convrot_fused_route(int64_t K, int64_t group);
+void launch_act_rows(const void* x, int x_dtype, int act, const void* w, float eps, int8_t* q, float* xs, void* y,
+                     int64_t M, int64_t K, bool recip, hipStream_t stream);
+void launch_convrot_quant_act(const void* x, int x_dtype, int act, const void* w, float eps, int8_t* q, float* xs,
+                              int64_t M, int64_t K, bool recip, hipStream_t stream);
 void launch_convrot_quant(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M, int64_t K,
                           bool recip, hipStream_t stream);
 void launch_convrot_rotate(const void* x, int x_dtype, void* y, int64_t M, int64_t K, int64_t G,
@@ -117,6 +121,14 @@ int check_convrot_group(int64_t K, int64_t group) {
         return fail(W8A8_ERR_VALUE, "features " + std::to_string(K) + " not divisible by group_size " +
                                         std::to_string(group));
     if (group > 16384) return fail(W8A8_ERR_RUNTIME, "ConvRot groups above 16384 are not supported");
+    return W8A8_OK;
+}
+
+// Input activation arguments (int8_linear.rs:37-97): a known code, and
+// RMSNorm's weight (ValueError text of :79-81).
+int check_act(int act, const void* act_weight) {
+    if (act < W8A8_ACT_NONE || act > W8A8_ACT_SITU) return fail(W8A8_ERR_VALUE, "unknown input activation code");
+    if (act == W8A8_ACT_RMSNORM && !act_weight) return fail(W8A8_ERR_VALUE, "input_act 'rms_norm' requires act_weight");
     return W8A8_OK;
 }
 
@@ -246,6 +258,64 @@ int w8a8_gated_residual(const void* x, const void* y, const void* gate0, const v
     w8a8::launch_gated_residual(x, y, prefix > 0 ? gate0 : gate1, gate1, out, batch, tokens, d, prefix, dtype,
                                 stream);
     return check_launch("gated_residual");
+}
+
+int w8a8_input_act(const void* x, int x_dtype, int act, const void* act_weight, double act_eps, void* y, int64_t M,
+                   int64_t K, hipStream_t stream) {
+    if (M < 0 || K < 0) return fail(W8A8_ERR_VALUE, "negative dimension");
+    if (int rc = check_act(act, act_weight)) return rc;
+    if (!valid_dtype(x_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for the input activation");
+    if (M == 0 || K == 0) return W8A8_OK;
+    if (!x || !y) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (act == W8A8_ACT_NONE) {
+        const int64_t bytes = M * K * (x_dtype == W8A8_F32 ? 4 : 2);
+        if (hipMemcpyAsync(y, x, bytes, hipMemcpyDeviceToDevice, stream) != hipSuccess) return check_launch("input_act");
+        return W8A8_OK;
+    }
+    w8a8::launch_act_rows(x, x_dtype, act, act_weight, static_cast<float>(act_eps), nullptr, nullptr, y, M, K, false,
+                          stream);
+    return check_launch("input_act");
+}
+
+int w8a8_quantize_rowwise_act(const void* x, int x_dtype, int act, const void* act_weight, double act_eps, int8_t* q,
+                              float* xs, int64_t M, int64_t K, int64_t convrot_group, uint32_t flags, void* aux,
+                              int64_t aux_bytes, hipStream_t stream) {
+    if (int rc = check_common(M, 0, K, flags)) return rc;
+    if (flags & ~W8A8_SCALE_RECIP) return fail(W8A8_ERR_VALUE, "w8a8_quantize_rowwise_act takes only W8A8_SCALE_RECIP");
+    if (int rc = check_act(act, act_weight)) return rc;
+    if (convrot_group) {
+        if (int rc = check_convrot_group(K, convrot_group)) return rc;
+    }
+    if (!valid_dtype(x_dtype)) return fail(W8A8_ERR_RUNTIME, "Unsupported input dtype for INT8 quantization");
+    if (M == 0) return W8A8_OK;
+    if (K > 0 && (!x || !q)) return fail(W8A8_ERR_VALUE, "null tensor pointer");
+    if (!xs) return fail(W8A8_ERR_VALUE, "null scale pointer");
+    const bool recip = flags & W8A8_SCALE_RECIP;
+    const float eps = static_cast<float>(act_eps);
+    if (act == W8A8_ACT_NONE) {
+        if (!convrot_group) return w8a8_quantize_rowwise(x, x_dtype, q, xs, M, K, flags, stream);
+        return w8a8_quantize_rowwise_convrot(x, x_dtype, q, xs, M, K, convrot_group, flags, aux, aux_bytes, stream);
+    }
+    if (K == 0) return w8a8_quantize_rowwise(x, x_dtype, q, xs, M, K, flags, stream);
+    if (!convrot_group) {
+        // the activation fused into the quantizer, with the crate's eager numerics
+        if (act == W8A8_ACT_GELU) return w8a8_quantize_rowwise(x, x_dtype, q, xs, M, K, flags | W8A8_ACT_GELU_TANH, stream);
+        w8a8::launch_act_rows(x, x_dtype, act, act_weight, eps, q, xs, nullptr, M, K, recip, stream);
+        return check_launch("quantize_int8_rowwise_act");
+    }
+    if (w8a8::convrot_fused_route(K, convrot_group)) {
+        // Kitchen's fused ConvRot quantizer with the activation in fp32
+        w8a8::launch_convrot_quant_act(x, x_dtype, act, act_weight, eps, q, xs, M, K, recip, stream);
+        return check_launch("quantize_int8_rowwise_convrot64");
+    }
+    // other groups: the eager activation into aux, rotated there in place, then quantized
+    if (!aux || aux_bytes < w8a8_convrot_workspace_bytes(M, K, convrot_group, x_dtype))
+        return fail(W8A8_ERR_VALUE, "aux buffer smaller than w8a8_convrot_workspace_bytes(M, K, group, dtype)");
+    w8a8::launch_act_rows(x, x_dtype, act, act_weight, eps, nullptr, nullptr, aux, M, K, false, stream);
+    if (int rc = check_launch("input_act")) return rc;
+    w8a8::launch_convrot_rotate(aux, x_dtype, aux, M, K, convrot_group, stream);
+    if (int rc = check_launch("convrot_rotate")) return rc;
+    return w8a8_quantize_rowwise(aux, x_dtype, q, xs, M, K, flags, stream);
 }
 
 int w8a8_row_scales(const void* x, int x_dtype, float* xs, int64_t M, int64_t K, uint32_t flags,
@@ -483,7 +553,8 @@ namespace {
 int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,
                      const void* bias, const w8a8::Residual* res, void* out, int out_dtype, int64_t M,
                      int64_t N, int64_t K, int64_t convrot_group, uint32_t flags, void* workspace,
-                     int64_t workspace_bytes, hipStream_t stream, const void* modulation = nullptr) {
+                     int64_t workspace_bytes, hipStream_t stream, const void* modulation = nullptr,
+                     int act = W8A8_ACT_NONE, const void* act_weight = nullptr, double act_eps = 0.0) {
     if (int rc = check_common(M, N, K, flags)) return rc;
     if (flags & W8A8_OUT_INT32) return fail(W8A8_ERR_VALUE, "W8A8_OUT_INT32 is a GEMM-only flag");
     if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
@@ -499,10 +570,12 @@ int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* w
         return fail(W8A8_ERR_RUNTIME,
                     "INT8 GEMM not supported on this GPU for these dimensions (requires SM >= 7.5, "
                     "and dimensions multiple of 4).");
+    if (int rc = check_act(act, act_weight)) return rc;
+    if (act != W8A8_ACT_NONE && (flags & W8A8_ACT_GELU_TANH))
+        return fail(W8A8_ERR_VALUE, "W8A8_ACT_GELU_TANH and an input activation code together");
     if (convrot_group) {
         if (int rc = check_convrot_group(K, convrot_group)) return rc;
-        if (flags & W8A8_ACT_GELU_TANH)
-            return fail(W8A8_ERR_VALUE, "an input activation with ConvRot is not supported by this library");
+        if (flags & W8A8_ACT_GELU_TANH) act = W8A8_ACT_GELU;   // the flag's GELU, on the ConvRot route
     }
     if (M == 0) return W8A8_OK;
     const int64_t need = convrot_group ? w8a8_int8_linear_convrot_workspace_bytes(M, K, convrot_group, x_dtype)
@@ -524,7 +597,8 @@ int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* w
     if (modulation) {
         if (int rc = w8a8_quantize_rowwise_modulated(x, x_dtype, modulation, q, xs, M, K, qflags, stream))
             return rc;
-    } else if (!convrot_group && !gemv && (flags & W8A8_FUSED_QUANT) && !(qflags & W8A8_ACT_GELU_TANH) &&
+    } else if (!convrot_group && act == W8A8_ACT_NONE && !gemv && (flags & W8A8_FUSED_QUANT) &&
+               !(qflags & W8A8_ACT_GELU_TANH) &&
                N > 0 && x_dtype != W8A8_F32 && K % 16 == 0) {
         if (int rc = w8a8_row_scales(x, x_dtype, xs, M, K, qflags, stream)) return rc;
         if (w8a8::launch_gemm_xq(x, x_dtype, xs, w, ws, ws_size, bias, out, out_dtype, M, N, K,
@@ -536,6 +610,13 @@ int int8_linear_impl(const void* x, int x_dtype, const int8_t* w, const float* w
     }
     if (modulation) {
         // quantized above
+    } else if (act != W8A8_ACT_NONE) {
+        void* aux = convrot_group ? static_cast<char*>(workspace) + (M * K + 255) / 256 * 256 + (M * 4 + 255) / 256 * 256
+                                  : nullptr;
+        const int64_t aux_bytes = convrot_group ? w8a8_convrot_workspace_bytes(M, K, convrot_group, x_dtype) : 0;
+        if (int rc = w8a8_quantize_rowwise_act(x, x_dtype, act, act_weight, act_eps, q, xs, M, K, convrot_group,
+                                               qflags & W8A8_SCALE_RECIP, aux, aux_bytes, stream))
+            return rc;
     } else if (convrot_group) {
         void* rotated = static_cast<char*>(workspace) + (M * K + 255) / 256 * 256 + (M * 4 + 255) / 256 * 256;
         if (int rc = w8a8_quantize_rowwise_convrot(x, x_dtype, q, xs, M, K, convrot_group, qflags, rotated,
@@ -587,6 +668,16 @@ int w8a8_int8_linear_modulated(const void* x, int x_dtype, const void* modulatio
     if (M > 0 && K > 0 && !modulation_scale) return fail(W8A8_ERR_VALUE, "null modulation_scale");
     return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, nullptr, out, out_dtype, M, N, K, 0, flags,
                             workspace, workspace_bytes, stream, modulation_scale ? modulation_scale : x);
+}
+
+int w8a8_int8_linear_act(const void* x, int x_dtype, int act, const void* act_weight, double act_eps, const int8_t* w,
+                         const float* ws, int64_t ws_size, const void* bias, const void* rscale, int64_t rscale_size,
+                         const void* resid, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                         int64_t convrot_group, uint32_t flags, void* workspace, int64_t workspace_bytes,
+                         hipStream_t stream) {
+    const w8a8::Residual res{rscale, rscale_size, resid};
+    return int8_linear_impl(x, x_dtype, w, ws, ws_size, bias, resid ? &res : nullptr, out, out_dtype, M, N, K,
+                            convrot_group, flags, workspace, workspace_bytes, stream, nullptr, act, act_weight, act_eps);
 }
 
 int w8a8_int8_linear_convrot(const void* x, int x_dtype, const int8_t* w, const float* ws, int64_t ws_size,

@@ -174,6 +174,68 @@ __device__ __forceinline__ uint32_t gelu_x2(uint32_t p) {
     else return gelu_f16_bits(p & 0xffffu) | (gelu_f16_bits(p >> 16) << 16);
 }
 
+// GELU of a value v already rounded to dtype T, as a float.
+template <int DT>
+__device__ __forceinline__ float gelu_value(float v) {
+    if constexpr (DT == W8A8_F32) return gelu_f32(v);
+    else return DType<DT>::load(static_cast<typename DType<DT>::storage>(gelu_bits<DT>(DType<DT>::store(v))));
+}
+
+// ---------------------------------------------------------------- input activations
+
+// Codes of the linear's input activation (Kitchen's input_act_codes.h; SiTU
+// is 4 as the crate passes it, inference/src/convrot.rs:211-238).  SwiGLU and
+// SiTU read a [gate | up] row twice as wide as the K they write.
+constexpr int kActNone = W8A8_ACT_NONE, kActGeluTanh = W8A8_ACT_GELU, kActSwiGLU = W8A8_ACT_SWIGLU,
+              kActRmsNorm = W8A8_ACT_RMSNORM, kActSiTU = W8A8_ACT_SITU;
+
+__host__ __device__ constexpr bool act_gated(int act) { return act == kActSwiGLU || act == kActSiTU; }
+
+// Correctly rounded fp32 exp and tanh (the double-precision function of the
+// fp32 argument, rounded once): ATen's CPU silu, sigmoid and tanh give these
+// values on every 16-bit input once rounded to the dtype.
+__device__ __forceinline__ float exp_cr(float v) { return static_cast<float>(exp(static_cast<double>(v))); }
+__device__ __forceinline__ float tanh_cr(float v) { return static_cast<float>(tanh(static_cast<double>(v))); }
+
+// The eager activations of the crate's apply_input (inference/src/int8_linear.rs:
+// 37-97): ATen ops on tensors of dtype T, each result rounded to T.  a is the
+// value (the gate for the gated ones), b the up value; the result is in T.
+template <int DT, int ACT>
+__device__ __forceinline__ float act_eager(float a, float b) {
+    using D = DType<DT>;
+    if constexpr (ACT == kActGeluTanh) {
+        return gelu_value<DT>(a);
+    } else if constexpr (ACT == kActSwiGLU) {
+        return D::round(D::round(a / (1.0f + exp_cr(-a))) * b);                   // silu(a) * b
+    } else if constexpr (ACT == kActSiTU) {
+        const float t4 = D::round(D::round(tanh_cr(D::round(b / 4.0f))) * 4.0f);  // tanh(b / 4) * 4
+        const float sg = D::round(1.0f / (1.0f + exp_cr(-b)));                   // sigmoid(b)
+        const float gated = D::round(t4 * sg);
+        const float t25 = D::round(D::round(tanh_cr(D::round(a / 25.0f))) * 25.0f);
+        return D::round(t25 * gated);
+    } else {
+        return a;
+    }
+}
+
+// The fused activations of Kitchen's ConvRot quantizer
+// (native/comfy-port/kitchen/int8_linear.cu:1175-1200,1230-1262): fp32, not
+// rounded to the dtype (RMSNorm is applied by the kernel from its row rstd).
+template <int ACT>
+__device__ __forceinline__ float act_fused(float a, float b) {
+    if constexpr (ACT == kActGeluTanh) {
+        const float kBeta = 0.79788456080286535588f;
+        const float inner = kBeta * (a + 0.044715f * a * a * a);
+        return 0.5f * a * (1.0f + tanh_cr(inner));
+    } else if constexpr (ACT == kActSwiGLU) {
+        return (a / (1.0f + exp_cr(-a))) * b;
+    } else if constexpr (ACT == kActSiTU) {
+        return (tanh_cr(a / 25.0f) * 25.0f) * ((tanh_cr(b / 4.0f) * 4.0f) * (1.0f / (1.0f + exp_cr(-b))));
+    } else {
+        return a;
+    }
+}
+
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
 // where an index selects a register array element (MFMA accumulators), so the
 // array can never be indexed dynamically (which would demote it to scratch).
@@ -296,13 +358,6 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d) {
 }
 
 // ---------------------------------------------------------------- epilogue
-
-// GELU of a value v already rounded to dtype T, as a float.
-template <int DT>
-__device__ __forceinline__ float gelu_value(float v) {
-    if constexpr (DT == W8A8_F32) return gelu_f32(v);
-    else return DType<DT>::load(static_cast<typename DType<DT>::storage>(gelu_bits<DT>(DType<DT>::store(v))));
-}
 
 // out = O( fma(float(acc) * xs, ws, bias) ), optional gelu on the O-rounded value.
 template <int ODT>

@@ -185,18 +185,44 @@ __global__ __launch_bounds__(1024) void convrot_quant_rows(const void* __restric
 }
 
 // Fused route, any alignment: one block per row, the rotated row in LDS
-// (K <= 16384 floats), stage by stage like the reference kernel.
-template <int DT>
+// (K <= 16384 floats), stage by stage like the reference kernel.  ACT fuses
+// an input activation the way that kernel does (int8_linear.cu:1175-1262): in
+// fp32, not rounded to T, x being [M, 2K] for the gated ones; RMSNorm scales
+// the row by its rstd and the weight w.
+template <int DT, int ACT>
 __global__ __launch_bounds__(256) void convrot_quant_rows_generic(const void* __restrict__ xv,
                                                                   int8_t* __restrict__ q,
                                                                   float* __restrict__ xs, int64_t M,
-                                                                  int K, int recip) {
+                                                                  int K, int recip, const void* __restrict__ wv,
+                                                                  float eps) {
     using D = DType<DT>;
+    using S = typename D::storage;
     extern __shared__ float rowbuf[];
     __shared__ float part[4];
+    __shared__ double dpart[4];
     const int64_t row = blockIdx.x;
-    const typename D::storage* x = static_cast<const typename D::storage*>(xv) + row * K;
-    for (int k = threadIdx.x; k < K; k += blockDim.x) rowbuf[k] = D::load(x[k]);
+    const int64_t in_w = act_gated(ACT) ? 2 * static_cast<int64_t>(K) : K;
+    const S* x = static_cast<const S*>(xv) + row * in_w;
+    float rstd = 1.0f;
+    if constexpr (ACT == kActRmsNorm) {
+        double acc = 0.0;
+        for (int k = threadIdx.x; k < K; k += blockDim.x) {
+            const double v = D::load(x[k]);
+            acc += v * v;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+        if ((threadIdx.x % kWave) == 0) dpart[threadIdx.x / kWave] = acc;
+        __syncthreads();
+        const double total = (dpart[0] + dpart[1]) + (dpart[2] + dpart[3]);
+        rstd = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(K)) + eps);
+    }
+    for (int k = threadIdx.x; k < K; k += blockDim.x) {
+        const float a = D::load(x[k]);
+        if constexpr (ACT == kActRmsNorm) rowbuf[k] = (a * rstd) * D::load(static_cast<const S*>(wv)[k]);
+        else if constexpr (act_gated(ACT)) rowbuf[k] = act_fused<ACT>(a, D::load(x[K + k]));
+        else rowbuf[k] = act_fused<ACT>(a, 0.0f);
+    }
     __syncthreads();
     for (int S = 1; S < kRotGroup; S *= 4) {
         for (int b = threadIdx.x; b < K / 4; b += blockDim.x) {
@@ -314,6 +340,18 @@ static int fused_rows_per_block(int ngroups) {
     return best;
 }
 
+// The row in LDS: up to 64 KB beside the kernel's static bytes.
+template <int DT, int ACT>
+static void launch_fused_generic(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, bool recip, const void* w,
+                                 float eps, hipStream_t stream) {
+    const size_t lds = K * sizeof(float);
+    if (lds > 32 * 1024)
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&convrot_quant_rows_generic<DT, ACT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    hipLaunchKernelGGL((convrot_quant_rows_generic<DT, ACT>), dim3(static_cast<unsigned>(M)), dim3(256), lds, stream,
+                       x, q, xs, M, static_cast<int>(K), recip ? 1 : 0, w, eps);
+}
+
 template <int DT>
 static void launch_fused(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, bool recip,
                          hipStream_t stream) {
@@ -329,14 +367,27 @@ static void launch_fused(const void* x, int8_t* q, float* xs, int64_t M, int64_t
         hipLaunchKernelGGL((convrot_quant_rows<DT>), grid, dim3(threads), quads * sizeof(float), stream, x, q,
                            xs, M, static_cast<int>(K), rpb, recip ? 1 : 0);
     } else {
-        // the row in LDS: up to 64 KB beside the kernel's static 16 bytes
-        const size_t lds = K * sizeof(float);
-        if (lds > 32 * 1024)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&convrot_quant_rows_generic<DT>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        hipLaunchKernelGGL((convrot_quant_rows_generic<DT>), dim3(static_cast<unsigned>(M)), dim3(256), lds,
-                           stream, x, q, xs, M, static_cast<int>(K), recip ? 1 : 0);
+        launch_fused_generic<DT, kActNone>(x, q, xs, M, K, recip, nullptr, 0.0f, stream);
     }
+}
+
+// Fused route with an input activation (act != 0): the LDS-row kernel.
+template <int DT>
+static void launch_fused_act(int act, const void* x, int8_t* q, float* xs, int64_t M, int64_t K, bool recip,
+                             const void* w, float eps, hipStream_t stream) {
+    switch (act) {
+        case kActGeluTanh: launch_fused_generic<DT, kActGeluTanh>(x, q, xs, M, K, recip, w, eps, stream); break;
+        case kActSwiGLU: launch_fused_generic<DT, kActSwiGLU>(x, q, xs, M, K, recip, w, eps, stream); break;
+        case kActRmsNorm: launch_fused_generic<DT, kActRmsNorm>(x, q, xs, M, K, recip, w, eps, stream); break;
+        default: launch_fused_generic<DT, kActSiTU>(x, q, xs, M, K, recip, w, eps, stream); break;
+    }
+}
+
+void launch_convrot_quant_act(const void* x, int x_dtype, int act, const void* w, float eps, int8_t* q, float* xs,
+                              int64_t M, int64_t K, bool recip, hipStream_t stream) {
+    if (x_dtype == W8A8_BF16) launch_fused_act<W8A8_BF16>(act, x, q, xs, M, K, recip, w, eps, stream);
+    else if (x_dtype == W8A8_F16) launch_fused_act<W8A8_F16>(act, x, q, xs, M, K, recip, w, eps, stream);
+    else launch_fused_act<W8A8_F32>(act, x, q, xs, M, K, recip, w, eps, stream);
 }
 
 void launch_convrot_quant(const void* x, int x_dtype, int8_t* q, float* xs, int64_t M, int64_t K,

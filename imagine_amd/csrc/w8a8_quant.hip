@@ -204,6 +204,103 @@ static void quant_dispatch_dt(const void* x, int8_t* q, float* xs, int64_t M, in
                        dim3(256), 0, stream, x, q, xs, M, K, recip);
 }
 
+// ---------------------------------------------------------------- input activations
+
+// Sum of a double over a 256-thread block (4 waves); part holds 4 doubles.
+__device__ __forceinline__ double block_sum_256(double v, double* part) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    if ((threadIdx.x % kWave) == 0) part[threadIdx.x / kWave] = v;
+    __syncthreads();
+    return (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+// 1 / sqrt(mean(x^2) + eps) of a row of K values, as ATen's rms_norm forms it
+// in fp32.  The squares are summed in double: exact for rows of ordinary
+// dynamic range, so the fp32 mean does not depend on the summation order.
+template <int DT>
+__device__ __forceinline__ float row_rstd(const typename DType<DT>::storage* x, int64_t K, float eps, double* part) {
+    double acc = 0.0;
+    for (int64_t k = threadIdx.x; k < K; k += blockDim.x) {
+        const double v = DType<DT>::load(x[k]);
+        acc += v * v;
+    }
+    const double total = block_sum_256(acc, part);
+    return 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(K)) + eps);
+}
+
+// The crate's eager input activation (inference/src/int8_linear.rs:37-97) of
+// one row per block of 256 threads: x is [M, K] ([M, 2K] for the gated
+// ones), the activated value of column k is act_eager (RMSNorm: T(x * rstd *
+// w)).  WRITE: store the activated [M, K] tensor in T (the ConvRot rotate
+// route rotates it next); else quantize it per token, two passes over the row
+// (the activation recomputed in the second), codes and scale as
+// quant_rows_generic.
+template <int DT, int ACT, bool WRITE>
+__global__ __launch_bounds__(256) void act_rows(const void* __restrict__ xv, const void* __restrict__ wv, float eps,
+                                                int8_t* __restrict__ q, float* __restrict__ xs,
+                                                void* __restrict__ yv, int64_t K, int recip) {
+    using D = DType<DT>;
+    using S = typename D::storage;
+    __shared__ double dpart[4];
+    __shared__ float part[4];
+    const int64_t row = blockIdx.x;
+    const int64_t in_w = act_gated(ACT) ? 2 * K : K;
+    const S* x = static_cast<const S*>(xv) + row * in_w;
+    float rstd = 1.0f;
+    if constexpr (ACT == kActRmsNorm) rstd = row_rstd<DT>(x, K, eps, dpart);
+    auto value = [&](int64_t k) -> float {
+        const float a = D::load(x[k]);
+        if constexpr (ACT == kActRmsNorm) return D::round((a * rstd) * D::load(static_cast<const S*>(wv)[k]));
+        else if constexpr (act_gated(ACT)) return act_eager<DT, ACT>(a, D::load(x[K + k]));
+        else return act_eager<DT, ACT>(a, 0.0f);
+    };
+    if constexpr (WRITE) {
+        S* y = static_cast<S*>(yv) + row * K;
+        for (int64_t k = threadIdx.x; k < K; k += blockDim.x) y[k] = D::store(value(k));
+    } else {
+        float amax = 0.0f;
+        for (int64_t k = threadIdx.x; k < K; k += blockDim.x) amax = fmaxf(amax, fabsf(value(k)));
+        amax = wave_max(amax);
+        if ((threadIdx.x % kWave) == 0) part[threadIdx.x / kWave] = amax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+        const float s = row_scale<DT>(amax, recip != 0);
+        if (threadIdx.x == 0) xs[row] = s;
+        const RowQuant rq = row_quant<DT>(s);
+        for (int64_t k = threadIdx.x; k < K; k += blockDim.x)
+            q[row * K + k] = static_cast<int8_t>(quant_elem<DT>(value(k), rq));
+    }
+}
+
+template <int DT, int ACT>
+static void act_rows_dt(const void* x, const void* w, float eps, int8_t* q, float* xs, void* y, int64_t M, int64_t K,
+                        int recip, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(M));
+    if (y) hipLaunchKernelGGL((act_rows<DT, ACT, true>), grid, dim3(256), 0, stream, x, w, eps, q, xs, y, K, recip);
+    else hipLaunchKernelGGL((act_rows<DT, ACT, false>), grid, dim3(256), 0, stream, x, w, eps, q, xs, y, K, recip);
+}
+
+template <int DT>
+static void act_rows_act(int act, const void* x, const void* w, float eps, int8_t* q, float* xs, void* y, int64_t M,
+                         int64_t K, int recip, hipStream_t stream) {
+    switch (act) {
+        case kActGeluTanh: act_rows_dt<DT, kActGeluTanh>(x, w, eps, q, xs, y, M, K, recip, stream); break;
+        case kActSwiGLU: act_rows_dt<DT, kActSwiGLU>(x, w, eps, q, xs, y, M, K, recip, stream); break;
+        case kActRmsNorm: act_rows_dt<DT, kActRmsNorm>(x, w, eps, q, xs, y, M, K, recip, stream); break;
+        default: act_rows_dt<DT, kActSiTU>(x, w, eps, q, xs, y, M, K, recip, stream); break;
+    }
+}
+
+// y != nullptr: write the activated [M, K] tensor to y; else quantize it to q, xs.
+void launch_act_rows(const void* x, int x_dtype, int act, const void* w, float eps, int8_t* q, float* xs, void* y,
+                     int64_t M, int64_t K, bool recip, hipStream_t stream) {
+    const int r = recip ? 1 : 0;
+    if (x_dtype == W8A8_BF16) act_rows_act<W8A8_BF16>(act, x, w, eps, q, xs, y, M, K, r, stream);
+    else if (x_dtype == W8A8_F16) act_rows_act<W8A8_F16>(act, x, w, eps, q, xs, y, M, K, r, stream);
+    else act_rows_act<W8A8_F32>(act, x, w, eps, q, xs, y, M, K, r, stream);
+}
+
 // ---------------------------------------------------------------- tensorwise
 
 // Tensorwise quantization: one scale for the whole tensor (the reference's

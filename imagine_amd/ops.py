@@ -10,9 +10,10 @@ of small operands (scales, bias) and supplies the current stream.
 The residual kwargs are fused into the GEMM / GEMV epilogue (or applied by
 the HIP residual kernel).  ``convrot`` rotates the activations by the regular
 Hadamard matrix of ``convrot_groupsize`` before quantizing them (fused into
-the quantizer on the crate's fused route).  Not built here (raise
-NotImplementedError): the SwiGLU / SiTU / RMSNorm input activations, and an
-input activation combined with ConvRot.
+the quantizer on the crate's fused route).  ``input_act`` is the crate's
+input activation (gelu_tanh, swiglu, situ, rms_norm with ``input_act_weight``
+and ``input_act_eps``), fused into the quantizer with the crate's eager
+numerics, or in fp32 into the ConvRot quantizer on its fused route.
 """
 import torch
 
@@ -87,6 +88,55 @@ def quantize_rowwise(x, scale_form="ieee", input_act=None):
     _lib.check(_lib.load().w8a8_quantize_rowwise(
         _ptr(x), _dtype_code(x.dtype, "INT8 quantization"), _ptr(q), _ptr(s), M, K, flags,
         _stream(x.device)))
+    return q, s
+
+
+def _act_args(x, input_act, weight, eps):
+    if input_act not in _lib.ACT_CODES:
+        raise ValueError(f"Unsupported input_act {input_act!r}")
+    act = _lib.ACT_CODES[input_act]
+    w = None
+    if act == 3:
+        if weight is None:
+            raise ValueError("input_act 'rms_norm' requires act_weight")
+        w = weight.to(device=x.device, dtype=x.dtype).reshape(-1).contiguous()
+    eps = torch.finfo(torch.float32).eps if eps is None else float(eps)
+    return act, w, eps
+
+
+def input_act(x, input_act, weight=None, eps=None):
+    """The crate's eager input activation (int8_linear.rs:37-97) of a [M, K]
+    (swiglu / situ: [M, 2K]) device tensor -> [M, K] in its dtype."""
+    _require_cuda(x)
+    x = _as_2d(x)
+    act, w, eps = _act_args(x, input_act, weight, eps)
+    M, width = x.shape
+    K = width // 2 if act in (2, 4) else width
+    y = torch.empty((M, K), dtype=x.dtype, device=x.device)
+    _lib.check(_lib.load().w8a8_input_act(_ptr(x), _dtype_code(x.dtype, "input activation"), act, _ptr(w), eps,
+                                          _ptr(y), M, K, _stream(x.device)))
+    return y
+
+
+def quantize_rowwise_act(x, input_act, weight=None, eps=None, convrot_group=0, scale_form="ieee"):
+    """Per-token quantization of the activated input -> (q [M, K], s [M, 1]),
+    by the crate's route: the eager activation fused into the quantizer, or
+    (convrot_group) the ConvRot quantizer with the activation fused in fp32 on
+    its fused route, else activated, rotated, then quantized."""
+    _require_cuda(x)
+    x = _as_2d(x)
+    act, w, eps = _act_args(x, input_act, weight, eps)
+    M, width = x.shape
+    K = width // 2 if act in (2, 4) else width
+    code = _dtype_code(x.dtype, "INT8 quantization")
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    aux_bytes = lib.w8a8_convrot_workspace_bytes(M, K, convrot_group, code) if convrot_group else 0
+    aux = torch.empty(max(aux_bytes, 1), dtype=torch.uint8, device=x.device) if aux_bytes > 0 else None
+    flags = _lib.SCALE_RECIP if scale_form == "recip" else 0
+    _lib.check(lib.w8a8_quantize_rowwise_act(_ptr(x), code, act, _ptr(w), eps, _ptr(q), _ptr(s), M, K, convrot_group,
+                                             flags, _ptr(aux), max(aux_bytes, 0), _stream(x.device)))
     return q, s
 
 
@@ -342,17 +392,35 @@ def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=Fals
     """
     if residual is not None and residual_scale is None:
         raise ValueError("int8_linear: residual requires residual_scale")
-    if input_act not in (None, "gelu_tanh"):
-        raise NotImplementedError(f"input_act {input_act!r} is not part of this build")
-    if convrot and input_act is not None:
-        raise NotImplementedError("an input activation combined with ConvRot is not part of this build")
+    if input_act not in _lib.ACT_CODES:
+        raise ValueError(f"Unsupported input_act {input_act!r}")
+    act = _lib.ACT_CODES[input_act]
     _require_cuda(x, weight)
     out_dtype = x.dtype if out_dtype is None else out_dtype
     shape = x.shape
     x2 = _as_2d(x)
     weight = weight.contiguous()
-    m, k = x2.shape
+    m, width = x2.shape
+    gated = act in (2, 4)  # swiglu / situ: [gate | up] rows (cuda_linear.rs:450-455)
+    k = width // 2 if gated else width
     n, kw = weight.shape
+    fused_act = bool(convrot) and act != 0 and convrot_groupsize == 256 and k % 256 == 0 and 256 <= k <= 16384
+    act_w = None
+    if act == 3:
+        if input_act_weight is None:
+            # the reference's texts by route (cuda_linear.rs:404-417,459-481,558-599)
+            if fused_act and m == 1:
+                raise RuntimeError("int8 fused convrot GEMV: rms_norm activation requires a weight")
+            if fused_act:
+                raise RuntimeError("INT8 rowwise convrot64 rms_norm weight must have K elements")
+            raise ValueError("input_act 'rms_norm' requires act_weight")
+        act_w = input_act_weight.to(device=x.device, dtype=x2.dtype).reshape(-1).contiguous()
+        if act_w.numel() != k:
+            raise RuntimeError("INT8 rowwise convrot64 rms_norm weight must have K elements")
+    if input_act_eps is None:
+        if act == 3 and fused_act:
+            raise TypeError("float() argument must be a string or a real number, not 'NoneType'")
+        input_act_eps = torch.finfo(torch.float32).eps  # ATen rms_norm's default (opmath epsilon)
     if k != kw:
         raise AssertionError("Input and weight inner dimensions must match")
     out_code = _dtype_code(out_dtype, "GEMV output")
@@ -375,9 +443,18 @@ def int8_linear(x, weight, weight_scale, bias=None, out_dtype=None, convrot=Fals
     if workspace is None or workspace.numel() < need or workspace.data_ptr() % 256 != 0:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
     flags = (_lib.SCALE_RECIP if scale_form == "recip" else 0) | (
-        _lib.ACT_GELU_TANH if input_act == "gelu_tanh" else 0) | (
+        _lib.ACT_GELU_TANH if input_act == "gelu_tanh" and not convrot else 0) | (
         _lib.FUSED_QUANT if fused_quant else 0)
-    if convrot:
+    if act in (2, 3, 4) or (convrot and act != 0):
+        r = rs = None
+        if residual is not None:
+            r, rs = _residual_operands(residual, residual_scale, m, n, x.device, out_dtype)
+        _lib.check(lib.w8a8_int8_linear_act(
+            _ptr(x2), x_code, act, _ptr(act_w), float(input_act_eps), _ptr(weight), _ptr(ws), ws.numel(), _ptr(b),
+            _ptr(rs), 0 if rs is None else rs.numel(), _ptr(r), _ptr(out), out_code, m, n, k,
+            convrot_groupsize if convrot else 0, flags & ~_lib.FUSED_QUANT, _ptr(workspace), workspace.numel(),
+            _stream(x.device)))
+    elif convrot:
         r = rs = None
         if residual is not None:
             r, rs = _residual_operands(residual, residual_scale, m, n, x.device, out_dtype)

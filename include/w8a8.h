@@ -59,6 +59,17 @@ extern "C" {
 #define W8A8_GIVEN_SCALE (1u << 5)   /* w8a8_quantize_tensorwise: *scale holds the scale
                                         to quantize with (the reference's scale argument) */
 
+/* Input activation codes of the linear (Kitchen's input_act_codes.h, SiTU 4
+ * as the crate passes it: inference/src/convrot.rs:211-238): the crate's
+ * int8_linear kwarg input_act = None, "gelu_tanh", "swiglu", "rms_norm", "situ"
+ * (inference/src/int8_linear.rs:37-97).  SwiGLU and SiTU take a [gate | up] row
+ * of 2K values and give K. */
+#define W8A8_ACT_NONE 0
+#define W8A8_ACT_GELU 1
+#define W8A8_ACT_SWIGLU 2
+#define W8A8_ACT_RMSNORM 3
+#define W8A8_ACT_SITU 4
+
 /* GEMM main loop (w8a8_gemm_dequant, w8a8_gemm_dequant_residual): flag bits
  * 8..11 hold a W8A8_GEMM_TILE_* code, W8A8_GEMM_TILE(code).  AUTO (0) lets
  * the shape choose; any other code requests that main loop, and a DMA tile
@@ -235,14 +246,58 @@ int w8a8_quantize_rowwise_convrot(const void* x, int x_dtype, int8_t* q, float* 
  * int8_linear kwargs, backend_signatures.rs:445-460; route cuda_linear.rs:586-599)
  * and an optional residual (resid == NULL: none).  The workspace holds q, xs
  * and, off the fused route, the rotated input:
- * w8a8_int8_linear_convrot_workspace_bytes gives its size.  Input activations
- * are not combined with ConvRot here (W8A8_ACT_GELU_TANH is refused). */
+ * w8a8_int8_linear_convrot_workspace_bytes gives its size.  W8A8_ACT_GELU_TANH
+ * is the gelu_tanh input activation (as w8a8_int8_linear_act). */
 int64_t w8a8_int8_linear_convrot_workspace_bytes(int64_t M, int64_t K, int64_t group, int x_dtype);
 int w8a8_int8_linear_convrot(const void* x, int x_dtype, const int8_t* w, const float* ws,
                              int64_t ws_size, const void* bias, const void* rscale,
                              int64_t rscale_size, const void* resid, void* out, int out_dtype,
                              int64_t M, int64_t N, int64_t K, int64_t group, uint32_t flags,
                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* ---- Input activations (the crate's input_act kwargs) ---------------------
+ * act is a W8A8_ACT_* code; act_weight is RMSNorm's [K] weight in x's dtype
+ * (NULL for the others; missing for rms_norm: W8A8_ERR_VALUE with the
+ * reference's text "input_act 'rms_norm' requires act_weight",
+ * int8_linear.rs:79-81), act_eps its epsilon.  K is the output width; x is
+ * [M, 2K] ([gate | up] rows) for SwiGLU and SiTU, [M, K] otherwise. */
+
+/* The eager activation of apply_input (inference/src/int8_linear.rs:37-97):
+ * ATen ops on x's dtype T, each result rounded to T:
+ *   gelu_tanh T(gelu(x)); swiglu T(T(silu(a)) * b);
+ *   situ T(T(T(tanh(T(a/25))) * 25) * T(T(T(tanh(T(b/4))) * 4) * T(sigmoid(b))));
+ *   rms_norm T(x * rstd * w), rstd = 1 / sqrt(mean(x^2) + eps)  (one rounding)
+ * with correctly rounded fp32 exp and tanh.  y is [M, K] in T. */
+int w8a8_input_act(const void* x, int x_dtype, int act, const void* act_weight, double act_eps, void* y, int64_t M,
+                   int64_t K, hipStream_t stream);
+
+/* The activation quantizer of the crate's int8_dispatch (cuda_linear.rs:
+ * 450-481, 586-619): q [M, K] int8 and xs [M] of act(x),
+ *   convrot_group == 0: the eager activation fused into the per-token
+ *     quantizer (same codes as w8a8_input_act then w8a8_quantize_rowwise);
+ *   ConvRot fused route (group 256, K % 256 == 0, 256 <= K <= 16384): Kitchen's
+ *     quantize_int8_rowwise_convrot64 with the activation fused in fp32 and not
+ *     rounded to T (native/comfy-port/kitchen/int8_linear.cu:1175-1262,
+ *     launcher :1618-1706; the crate's predicate cuda_linear.rs:404-417);
+ *   other ConvRot groups: the eager activation, rotated, quantized; aux then
+ *     holds w8a8_convrot_workspace_bytes(M, K, group, x_dtype) bytes.
+ * Flags: W8A8_SCALE_RECIP. */
+int w8a8_quantize_rowwise_act(const void* x, int x_dtype, int act, const void* act_weight, double act_eps, int8_t* q,
+                              float* xs, int64_t M, int64_t K, int64_t convrot_group, uint32_t flags, void* aux,
+                              int64_t aux_bytes, hipStream_t stream);
+
+/* The operator with every kwarg of the crate's int8_linear
+ * (backend_signatures.rs:445-460; int8_dispatch cuda_linear.rs:419-824):
+ * input activation, ConvRot (convrot_group 0: none) and residual (resid NULL:
+ * none) in one call.  Routes as w8a8_int8_linear on the output width K.
+ * Workspace: w8a8_int8_linear_workspace_bytes(M, K) without ConvRot,
+ * w8a8_int8_linear_convrot_workspace_bytes(M, K, group, x_dtype) with it.
+ * Flags: W8A8_SCALE_RECIP, W8A8_ROUTE_GEMM. */
+int w8a8_int8_linear_act(const void* x, int x_dtype, int act, const void* act_weight, double act_eps, const int8_t* w,
+                         const float* ws, int64_t ws_size, const void* bias, const void* rscale, int64_t rscale_size,
+                         const void* resid, void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                         int64_t convrot_group, uint32_t flags, void* workspace, int64_t workspace_bytes,
+                         hipStream_t stream);
 
 /* ---- Weight quantizers (TensorWiseINT8Layout.from_float) -----------------
  * The layout's quantize step (inference/src/layout_complete.rs:119-160):

@@ -50,6 +50,8 @@ def lib():
         f.w8o_gelu_tanh.restype = ctypes.c_float
         f.w8o_tanh_cr.argtypes = [ctypes.c_float]
         f.w8o_tanh_cr.restype = ctypes.c_float
+        f.w8o_input_act.argtypes = [p, i32, i64, i64, i32, p, ctypes.c_float, p]
+        f.w8o_convrot_quant_act.argtypes = [p, i32, i64, i64, i64, i32, i32, p, ctypes.c_float, p, p, p]
         f.w8o_round_to.argtypes = [ctypes.c_float, i32]
         f.w8o_round_to.restype = ctypes.c_float
     return _lib
@@ -141,6 +143,42 @@ def convrot_quant(x, dtype, group, scale_mode=0):
     work = np.empty((K,), np.float32)
     lib().w8o_convrot_quant(_ptr(x), DTYPE_CODE[dtype], M, K, group, scale_mode, _ptr(q), _ptr(s),
                             _ptr(work))
+    return q, s
+
+
+ACT_CODE = {None: 0, "gelu_tanh": 1, "swiglu": 2, "rms_norm": 3, "situ": 4}
+
+
+def input_act(x, dtype, act, weight=None, eps=0.0):
+    """The eager input activation (int8_linear.rs:37-97) of [M, K] (or [M, 2K]
+    for swiglu / situ) storage -> [M, K] storage of the dtype."""
+    x = np.ascontiguousarray(x, dtype=_storage(dtype))
+    code = ACT_CODE[act]
+    M = x.shape[0]
+    K = x.shape[1] // 2 if code in (2, 4) else x.shape[1]
+    y = np.empty((M, K), _storage(dtype))
+    wt = None if weight is None else np.ascontiguousarray(weight, dtype=_storage(dtype))
+    lib().w8o_input_act(_ptr(x), DTYPE_CODE[dtype], M, K, code, _ptr(wt), float(eps), _ptr(y))
+    return y
+
+
+def convrot_quant_act(x, dtype, group, act, weight=None, eps=0.0, scale_mode=0):
+    """ConvRot quantization with an input activation, by the reference's route:
+    on the fused route the activation is fused in fp32 (int8_linear.cu:1175-1262),
+    elsewhere it is applied eagerly (rounded to the dtype) before the rotation."""
+    x = np.ascontiguousarray(x, dtype=_storage(dtype))
+    code = ACT_CODE[act]
+    M = x.shape[0]
+    K = x.shape[1] // 2 if code in (2, 4) else x.shape[1]
+    if code == 0 or not convrot_fused_route(K, group):
+        xa = x if code == 0 else input_act(x, dtype, act, weight, eps)
+        return convrot_quant(xa, dtype, group, scale_mode=scale_mode)
+    q = np.empty((M, K), np.int8)
+    s = np.empty((M,), np.float32)
+    work = np.empty((K,), np.float32)
+    wt = None if weight is None else np.ascontiguousarray(weight, dtype=_storage(dtype))
+    lib().w8o_convrot_quant_act(_ptr(x), DTYPE_CODE[dtype], M, K, group, scale_mode, code, _ptr(wt), float(eps),
+                                _ptr(q), _ptr(s), _ptr(work))
     return q, s
 
 

@@ -30,6 +30,12 @@
  *                        eager residual modes of the GEMM, GEMV and M=1 routes).
  *   w8o_quant_tensorwise reference tensorwise golden vectors
  *                        (reference_primitives.py:357-365, deterministic cases).
+ *   w8o_input_act        every 16-bit input of silu / sigmoid / tanh against ATen;
+ *                        the SwiGLU and SiTU op chains against ATen on random
+ *                        pairs; rms_norm against ATen within one ulp; the
+ *                        reference's swiglu / situ / rms_norm CUDA payloads.
+ *   w8o_convrot_quant_act the reference's ConvRot + activation CUDA payloads
+ *                        (fast-math exp / tanh there: see the function).
  *   w8o_convrot_*        reference ConvRot CUDA payloads (fused group-256 route
  *                        and rotate-then-quantize route); the stage order against
  *                        a dense float64 Hadamard matmul (H built by Kronecker
@@ -289,6 +295,118 @@ void w8o_convrot_quant(const void* x, int dtype, int64_t M, int64_t K, int64_t G
         float amax = 0.0f;
         for (int64_t k = 0; k < K; ++k) work[k] = load_as_f32(x, dtype, m * K + k);
         for (int64_t g = 0; g < K; g += G) fht_group(work + g, G);
+        for (int64_t k = 0; k < K; ++k) {
+            float a = fabsf(work[k]);
+            if (a > amax) amax = a;
+        }
+        const float scale = row_scale(amax, dtype, scale_mode);
+        s[m] = scale;
+        const float sT = scale_in_dtype(scale, dtype);
+        for (int64_t k = 0; k < K; ++k) q[m * K + k] = quant_value(round_to(work[k], dtype), sT, dtype);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Input activations of the linear (act codes of Kitchen's input_act_codes.h,
+ * SiTU = 4 as the crate passes it, convrot.rs:211-238):
+ *   0 none, 1 gelu_tanh, 2 swiglu, 3 rms_norm, 4 situ.
+ * SwiGLU and SiTU read a [gate | up] row twice as wide as the K they write.
+ * exp and tanh are the correctly rounded fp32 values (double evaluation
+ * rounded once); ATen's CPU silu, sigmoid and tanh equal them on every 16-bit
+ * input (tests/test_oracle.py). */
+static float exp_cr(float v) { return (float)exp((double)v); }
+static float tanh_cr(float v) { return (float)tanh((double)v); }
+
+/* Mean of squares of a row: the squares of 16-bit or fp32 values are exact in
+ * double and their double sum is exact for rows of ordinary dynamic range, so
+ * this is the exact mean rounded once to fp32 (any summation order gives it). */
+static float row_mean_sq(const void* x, int dtype, int64_t base, int64_t K) {
+    double acc = 0.0;
+    for (int64_t k = 0; k < K; ++k) {
+        const double v = (double)load_as_f32(x, dtype, base + k);
+        acc += v * v;
+    }
+    return (float)(acc / (double)K);
+}
+
+/* The eager form (inference/src/int8_linear.rs:37-97): ATen ops on tensors of
+ * the input dtype, each result rounded to it:
+ *   gelu_tanh  T(gelu(x))
+ *   swiglu     T(T(silu(a)) * b),  silu(a) = a / (1 + exp(-a))
+ *   situ       T(T(T(tanh(T(a / 25))) * 25) * T(T(T(tanh(T(b / 4))) * 4) * T(sigmoid(b))))
+ *   rms_norm   T(x * rstd * T(w)),  rstd = 1 / sqrt(mean(x^2) + eps)   (ATen's
+ *              fused rms_norm: the weight applied in fp32, one rounding)
+ * x is [M, K] or [M, 2K]; y is [M, K] in the dtype; weight [K] in the dtype. */
+void w8o_input_act(const void* x, int dtype, int64_t M, int64_t K, int act, const void* weight, float eps,
+                   void* y) {
+    const int64_t in_w = (act == 2 || act == 4) ? 2 * K : K;
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t base = m * in_w;
+        float rstd = 1.0f;
+        if (act == 3) rstd = 1.0f / sqrtf(row_mean_sq(x, dtype, base, K) + eps);
+        for (int64_t k = 0; k < K; ++k) {
+            const float a = load_as_f32(x, dtype, base + k);
+            float v = a;
+            if (act == 1) {
+                v = round_to(w8o_gelu_tanh(a), dtype);
+            } else if (act == 2) {
+                const float b = load_as_f32(x, dtype, base + K + k);
+                v = round_to(round_to(a / (1.0f + exp_cr(-a)), dtype) * b, dtype);
+            } else if (act == 4) {
+                const float b = load_as_f32(x, dtype, base + K + k);
+                const float t4 = round_to(round_to(tanh_cr(round_to(b / 4.0f, dtype)), dtype) * 4.0f, dtype);
+                const float sg = round_to(1.0f / (1.0f + exp_cr(-b)), dtype);
+                const float gated = round_to(t4 * sg, dtype);
+                const float t25 = round_to(round_to(tanh_cr(round_to(a / 25.0f, dtype)), dtype) * 25.0f, dtype);
+                v = round_to(t25 * gated, dtype);
+            } else if (act == 3) {
+                v = round_to((a * rstd) * load_as_f32(weight, dtype, k), dtype);
+            }
+            store_from_f32(y, dtype, m * K + k, v);
+        }
+    }
+}
+
+/* The fused form inside the ConvRot quantizer
+ * (native/comfy-port/kitchen/int8_linear.cu:1175-1200,1230-1262): the activated
+ * value stays in fp32 (no rounding to the dtype) and feeds the rotation:
+ *   gelu_tanh  0.5 v (1 + tanh(sqrt(2/pi) (v + ((0.044715 v) v) v)))
+ *   swiglu     (g / (1 + exp(-g))) * u
+ *   situ       (tanh(a / 25) * 25) * ((tanh(b / 4) * 4) * (1 / (1 + exp(-b))))
+ *   rms_norm   (v * rstd) * w,  rstd = 1 / sqrt(mean(v^2) + eps)
+ * The reference compiles it with fast-math exp / tanh / rsqrt, which no
+ * fixture tells from these correctly rounded ones (parity unpinned there). */
+static float fused_act(const void* x, int dtype, int64_t base, int64_t K, int64_t k, int act,
+                       const void* weight, float rstd) {
+    const float a = load_as_f32(x, dtype, base + k);
+    if (act == 1) {
+        const float kBeta = (float)(1.41421356237309504880 * 1.12837916709551257390 * 0.5);
+        const float inner = kBeta * (a + 0.044715f * a * a * a);
+        return 0.5f * a * (1.0f + tanh_cr(inner));
+    }
+    if (act == 2) {
+        const float u = load_as_f32(x, dtype, base + K + k);
+        return (a / (1.0f + exp_cr(-a))) * u;
+    }
+    if (act == 4) {
+        const float b = load_as_f32(x, dtype, base + K + k);
+        return (tanh_cr(a / 25.0f) * 25.0f) * ((tanh_cr(b / 4.0f) * 4.0f) * (1.0f / (1.0f + exp_cr(-b))));
+    }
+    if (act == 3) return (a * rstd) * load_as_f32(weight, dtype, k);
+    return a;
+}
+
+/* w8o_convrot_quant with a fused input activation: x is [M, K] or [M, 2K]. */
+void w8o_convrot_quant_act(const void* x, int dtype, int64_t M, int64_t K, int64_t G, int scale_mode, int act,
+                           const void* weight, float eps, int8_t* q, float* s, float* work) {
+    const int64_t in_w = (act == 2 || act == 4) ? 2 * K : K;
+    for (int64_t m = 0; m < M; ++m) {
+        const int64_t base = m * in_w;
+        float rstd = 1.0f;
+        if (act == 3) rstd = 1.0f / sqrtf(row_mean_sq(x, dtype, base, K) + eps);
+        for (int64_t k = 0; k < K; ++k) work[k] = fused_act(x, dtype, base, K, k, act, weight, rstd);
+        for (int64_t g = 0; g < K; g += G) fht_group(work + g, G);
+        float amax = 0.0f;
         for (int64_t k = 0; k < K; ++k) {
             float a = fabsf(work[k]);
             if (a > amax) amax = a;

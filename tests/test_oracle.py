@@ -23,6 +23,11 @@ def _to_torch(storage, dtype):
     return t if dtype == "f32" else t.view(torch.int16).view(TORCH_DTYPE[dtype])
 
 
+def _storage(t, dtype):
+    t = t.contiguous()
+    return t.numpy() if dtype == "f32" else t.view(torch.int16).numpy().view(np.uint16)
+
+
 def _tie_patterns(low_bits):
     """All float32 bit patterns whose low bits below the 16-bit mantissa cut
     equal one of the given values (ties, just below/above ties, exact)."""
@@ -434,3 +439,101 @@ def test_convrot_scale_form_is_distinguished_on_the_rotate_route():
             continue
         misses[O.convrot_fused_route(c["shape"][-1], c["group"])] += not np.array_equal(got, want)
     assert misses[True] == 0 and misses[False] > 0
+
+
+# ---------------------------------------------------------------- input activations
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_input_act_swiglu_and_situ_equal_aten_op_chains(dtype):
+    """The eager SwiGLU and SiTU (int8_linear.rs:44-75) against the ATen op
+    chains the crate issues, on every 16-bit gate value (with a few up values)
+    and on random pairs: bit for bit."""
+    td = {"bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    bits = bits[np.isfinite(O.to_f32(bits, dtype))]
+    g = torch.Generator().manual_seed(12)
+    rand_a = (torch.randn(50000, generator=g) * 20).to(td).view(torch.int16).numpy().view(np.uint16)
+    rand_b = (torch.randn(50000, generator=g) * 5).to(td).view(torch.int16).numpy().view(np.uint16)
+    for ups in (1.0, -1.5, 3.25):
+        up = np.full(bits.shape, O.to_dtype(np.float32([ups]), dtype)[0], np.uint16)
+        pairs = [(bits, up), (up, bits), (rand_a, rand_b)]
+        for a, b in pairs:
+            at, bt = _to_torch(a, dtype), _to_torch(b, dtype)
+            sw = (torch.nn.functional.silu(at) * bt).view(torch.int16).numpy().view(np.uint16)
+            gated = (bt / 4.).tanh_().mul_(4.).mul_(bt.sigmoid())
+            si = (at / 25.).tanh_().mul_(25.).mul_(gated).view(torch.int16).numpy().view(np.uint16)
+            row = np.concatenate([a, b])[None, :]
+            assert np.array_equal(O.input_act(row, dtype, "swiglu")[0], sw)
+            assert np.array_equal(O.input_act(row, dtype, "situ")[0], si)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_input_act_rms_norm_within_one_ulp_of_aten(dtype):
+    """rms_norm with a weight (int8_linear.rs:77-95) against ATen's: within one
+    ulp for 16-bit outputs, two for fp32 (ATen sums the squares in fp32 in its
+    own order; the oracle's mean is the exactly rounded one), mostly
+    bit-equal."""
+    td = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    g = torch.Generator().manual_seed(13)
+    x = (torch.randn(64, 3072, generator=g) * 3).to(td)
+    w = (1 + 0.2 * torch.randn(3072, generator=g)).to(td)
+    ref = torch.nn.functional.rms_norm(x, [3072], w, 1e-6)
+    got = O.input_act(_storage(x, dtype), dtype, "rms_norm", _storage(w, dtype), 1e-6)
+    a = O.to_f32(got, dtype).astype(np.float64)
+    b = ref.float().numpy().astype(np.float64)
+    rel = {"bf16": 2.0**-7, "f16": 2.0**-10, "f32": 2.0**-21}[dtype]   # fp32: two ulps (rsqrt rounding)
+    assert (np.abs(a - b) <= np.abs(b) * rel).all()
+    assert (got.reshape(-1) == _storage(ref, dtype).reshape(-1)).mean() > (0.97 if dtype != "f32" else 0.7)
+
+
+def _activation_chain(c, ops):
+    """The crate's route for an activation case (cuda_linear.rs:450-481,586-619)
+    on the oracle, CUDA scale form."""
+    xd, od = OP.dtype_name(c["dtype"]), OP.dtype_name(c["output_dtype"])
+    act, k, n, group = c.get("activation"), c["weight_k"], c["n"], c["group"]
+    x = O.to_dtype(ops["x"].reshape(-1, ops["x"].shape[-1]), xd)
+    weight = O.to_dtype(np.ones(k, np.float32), xd) if act == "rms_norm" else None
+    if c["convrot"]:
+        q, s = O.convrot_quant_act(x, xd, group, act, weight, 0.0, scale_mode=1)
+    else:
+        q, s = O.quant_rowwise(O.input_act(x, xd, act, weight, 0.0) if act else x, xd, scale_mode=1)
+    acc = O.gemm_i32(q, ops["weight"])
+    bias = None if ops["bias"] is None else O.to_dtype(ops["bias"], od)
+    out = O.epilogue_kitchen(acc, s, ops["scale"].astype(np.float32), bias, od)
+    if ops["residual"] is not None:
+        out = O.residual(out, O.to_dtype(ops["residual"].reshape(-1, n), od), O.to_dtype(ops["residual_scale"], od), od)
+    return out.reshape(-1), FX.payload(c, od), od
+
+
+def test_activation_payloads_reproduce_on_the_oracle():
+    """The reference's swiglu / situ / rms_norm / gelu CUDA payloads
+    (plain and bias + residual modes), routed as the crate routes them:
+      * eager route (no ConvRot, or ConvRot off its fused route), 16-bit
+        inputs: every case bit for bit;
+      * fp32 inputs on the eager route: ATen's vectorised exp / tanh differ
+        from the correctly rounded ones in the last bits: within 4e-6;
+      * the fused ConvRot route: Kitchen's kernel uses fast-math exp / tanh /
+        rsqrt (parity unpinned there): 16-bit RMSNorm bit for bit, the rest
+        within 4e-4 of the largest output."""
+    counts = {"exact": 0, "fp32_close": 0, "fused_close": 0}
+    for c in FX.load()["cuda_int8_activation"]:
+        if "error" in c or c.get("activation") is None:
+            continue
+        got, want, od = _activation_chain(c, OP.activation_operands(c))
+        fused = c["convrot"] and O.convrot_fused_route(c["weight_k"], c["group"])
+        xd = OP.dtype_name(c["dtype"])
+        if np.array_equal(got, want):
+            counts["exact"] += 1
+            continue
+        a, b = O.to_f32(got, od).astype(np.float64), O.to_f32(want, od).astype(np.float64)
+        err = np.abs(a - b).max() / np.abs(b).max()
+        if fused:
+            assert not (c["activation"] == "rms_norm" and xd != "f32"), c
+            assert err <= 4e-4, (c, err)
+            counts["fused_close"] += 1
+        else:
+            assert xd == "f32", c
+            assert err <= 4e-6, (c, err)
+            counts["fp32_close"] += 1
+    assert counts["exact"] >= 600, counts
