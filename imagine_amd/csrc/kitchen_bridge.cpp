@@ -19,6 +19,7 @@
 // Scale form: these names stand in for Kitchen's CUDA kernels, so the row
 // scale is their amax * (1/127) (W8A8_SCALE_RECIP, int8_linear.cu:205-208).
 #include <ATen/core/Tensor.h>
+#include <ATen/ops/empty.h>
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
@@ -322,12 +323,14 @@ int64_t dequantize_int8_linear(const Args& g) {
 // act_eps, stream, residual, residual_scale) -- the crate's 16-argument list
 // (cuda_linear.rs:558-582; the pinned 11-argument wrapper,
 // dlpack_bindings.cpp:3594-3660, without the activation and residual ones, is
-// taken too): quantize into q_scratch / x_scales, then the M = 1 GEMV.
+// taken too): quantize into q_scratch / x_scales, then the M = 1 GEMV.  The
+// crate sends activation codes on the ConvRot route only (cuda_linear.rs:
+// 525-529); they are fused into the rotation in fp32.
 int64_t int8_linear_m1(const Args& g) {
     const bool full = g.n == 16;
     const at::Tensor& x = dense(ranked(g.tensor(0), 2), "input");
-    const at::Tensor& q = dense(typed(ranked(g.tensor(1), 2), at::kChar), "q_scratch");
-    const at::Tensor& xs = dense(typed(ranked(g.tensor(2), 2), at::kFloat), "x_scales");
+    const at::Tensor& q = dense(typed(g.tensor(1), at::kChar), "q_scratch");
+    const at::Tensor& xs = dense(typed(g.tensor(2), at::kFloat), "x_scales");
     const at::Tensor& w = dense(typed(ranked(g.tensor(3), 2), at::kChar), "weight");
     const at::Tensor& ws = dense(typed(g.tensor(4), at::kFloat), "weight_scales");
     const at::Tensor* bias = g.optional_tensor(5);
@@ -337,7 +340,9 @@ int64_t int8_linear_m1(const Args& g) {
     const int64_t group = g.integer(9);
     const int64_t act = full ? g.integer(10) : 0;
     const int64_t st = g.integer(full ? 13 : 10);
-    const int64_t M = x.size(0), K = x.size(1), N = w.size(0);
+    // gated activations take [gate | up] rows of twice the weight's K
+    const int64_t M = x.size(0), N = w.size(0);
+    const int64_t K = x.size(1) / ((act == W8A8_ACT_SWIGLU || act == W8A8_ACT_SITU) ? 2 : 1);
     if (M != 1) throw std::runtime_error("INT8 M=1 linear expects input M == 1");
     if (w.size(1) != K) throw std::runtime_error("INT8 M=1 linear weight K mismatch");
     if (out.size(0) != 1 || out.size(1) != N) throw std::runtime_error("INT8 M=1 linear output shape mismatch");
@@ -346,24 +351,37 @@ int64_t int8_linear_m1(const Args& g) {
         throw std::runtime_error("INT8 M=1 ConvRot linear requires group_size 256 and K divisible by 256");
     const int code = dtype_code(x);
     if (code < 0) throw std::runtime_error("Unsupported input dtype for INT8 M=1 linear");
-    if (act != 0) throw std::runtime_error("INT8 M=1 linear: input activations are not part of this library");
-    // the crate passes empty scratch tensors on the ConvRot route; the
-    // quantizer needs [1, K] codes and a [1, 1] scale
-    if (q.numel() < K || xs.numel() < 1)
-        throw std::runtime_error("INT8 M=1 linear: this library needs q_scratch [1, K] and x_scales [1, 1]");
-    if (!convrot && (q.size(0) != 1 || q.size(1) != K)) throw std::runtime_error("INT8 M=1 linear q scratch shape mismatch");
-    if (!convrot && (xs.size(0) != 1 || xs.size(1) != 1))
+    if (act != 0 && !convrot) throw std::runtime_error("INT8 M=1 linear: input activations need the ConvRot route");
+    const at::Tensor* aw = full ? g.optional_tensor(11) : nullptr;
+    const bool has_w = aw && aw->numel() > 0;
+    if (act == W8A8_ACT_RMSNORM && (!has_w || aw->numel() != K))
+        throw std::runtime_error("int8 fused convrot GEMV: rms_norm activation requires a weight");
+    // the crate passes empty scratch tensors on the ConvRot route (Kitchen
+    // fuses that quantizer into its GEMV); here the codes and the scale go
+    // through [1, K] / [1, 1] buffers taken from torch's allocator on the
+    // current stream, which is the stream the crate passes
+    at::Tensor q_own, xs_own;
+    const bool own = convrot && (q.numel() < K || xs.numel() < 1);
+    if (own) {
+        q_own = at::empty({1, K}, x.options().dtype(at::kChar));
+        xs_own = at::empty({1, 1}, x.options().dtype(at::kFloat));
+    }
+    if (!convrot && (q.dim() != 2 || q.size(0) != 1 || q.size(1) != K))
+        throw std::runtime_error("INT8 M=1 linear q scratch shape mismatch");
+    if (!convrot && (xs.dim() != 2 || xs.size(0) != 1 || xs.size(1) != 1))
         throw std::runtime_error("INT8 M=1 linear activation scale shape mismatch");
     if (dtype_code(out) != out_code) throw std::runtime_error("INT8 M=1 linear output dtype does not match its code");
     const int oc = static_cast<int>(out_code);
     const void* b = bias_ptr(bias, N, oc, "INT8 M=1 linear bias shape mismatch", "Unsupported bias dtype for INT8 M=1 linear");
     const Residual r = full ? residual_of(g.optional_tensor(14), g.optional_tensor(15), 1, N, oc, "int8_linear_m1")
                             : Residual{};
-    auto* qp = static_cast<int8_t*>(q.data_ptr());
-    auto* xsp = static_cast<float*>(xs.data_ptr());
+    auto* qp = static_cast<int8_t*>(own ? q_own.data_ptr() : q.data_ptr());
+    auto* xsp = static_cast<float*>(own ? xs_own.data_ptr() : xs.data_ptr());
     const hipStream_t s = stream_of(st);
     if (convrot)
-        abi(w8a8_quantize_rowwise_convrot(x.data_ptr(), code, qp, xsp, 1, K, 256, W8A8_SCALE_RECIP, nullptr, 0, s));
+        abi(w8a8_quantize_rowwise_act(x.data_ptr(), code, static_cast<int>(act),
+                                      has_w ? dense(*aw, "act_weight").data_ptr() : nullptr, full ? g.real(12) : 0.0, qp,
+                                      xsp, 1, K, 256, W8A8_SCALE_RECIP, nullptr, 0, s));
     else
         abi(w8a8_quantize_rowwise(x.data_ptr(), code, qp, xsp, 1, K, W8A8_SCALE_RECIP, s));
     auto* wp = static_cast<const int8_t*>(w.data_ptr());
@@ -373,6 +391,44 @@ int64_t int8_linear_m1(const Args& g) {
                                        out.data_ptr(), oc, 1, N, K, 0, s));
     else
         abi(w8a8_gemv_dequant(qp, wp, xsp, wsp, ws.numel(), b, out.data_ptr(), oc, 1, N, K, 0, s));
+    return 0;
+}
+
+// quantize_int8_rowwise_convrot64(input, output, scales, group_size,
+// stochastic, act_code, seed, act_weight, act_eps, stream): the crate's fused
+// ConvRot quantizer with an optional input activation (convrot.rs:169-206;
+// dlpack_bindings.cpp:3430-3483, SiTU's code 4 and width as the crate passes
+// them).  Activations fused in fp32 as Kitchen's kernel does.
+int64_t quantize_int8_rowwise_convrot64(const Args& g) {
+    const at::Tensor& x = dense(ranked(g.tensor(0), 2), "input");
+    const at::Tensor& q = dense(typed(ranked(g.tensor(1), 2), at::kChar), "output");
+    const at::Tensor& s = dense(typed(ranked(g.tensor(2), 2), at::kFloat), "scales");
+    const int64_t group = g.integer(3);
+    const bool stochastic = g.integer(4) != 0;
+    const int64_t act = g.integer(5);
+    (void)g.integer(6);
+    const at::Tensor* aw = g.optional_tensor(7);
+    const double eps = g.real(8);
+    const int64_t M = x.size(0), K = q.size(1);
+    const int64_t in_width = (act == W8A8_ACT_SWIGLU || act == W8A8_ACT_SITU) ? 2 : 1;
+    if (q.size(0) != M || x.size(1) != K * in_width) throw std::runtime_error("INT8 rowwise convrot64 output shape mismatch");
+    if (s.size(0) != M || s.size(1) != 1) throw std::runtime_error("INT8 rowwise convrot64 scale shape mismatch");
+    const int code = dtype_code(x);
+    if (code < 0) throw std::runtime_error("Unsupported input dtype for INT8 rowwise convrot64 quantization");
+    const bool has_w = aw && aw->numel() > 0;
+    if (act == W8A8_ACT_RMSNORM) {
+        if (!has_w || aw->numel() != K) throw std::runtime_error("INT8 rowwise convrot64 rms_norm weight must have K elements");
+        if (dtype_code(*aw) != code) throw std::runtime_error("INT8 rowwise convrot64 rms_norm weight dtype must match the input");
+    }
+    if (act < W8A8_ACT_NONE || act > W8A8_ACT_SITU) throw std::runtime_error("Unknown INT8 input activation code");
+    if (stochastic) throw std::runtime_error("stochastic INT8 rounding is not part of this library");
+    // Kitchen's kernel rotates 256-wide groups whatever group_size says; the
+    // crate only takes this route with group 256 (cuda_linear.rs:404-417)
+    if (group != 256 || K % 256 != 0 || K < 256 || K > 16384)
+        throw std::runtime_error("INT8 rowwise convrot64 needs group 256 and K a multiple of 256 up to 16384");
+    abi(w8a8_quantize_rowwise_act(x.data_ptr(), code, static_cast<int>(act), has_w ? dense(*aw, "act_weight").data_ptr() : nullptr,
+                                  eps, static_cast<int8_t*>(q.data_ptr()), static_cast<float*>(s.data_ptr()), M, K, 256,
+                                  W8A8_SCALE_RECIP, nullptr, 0, stream_of(g.integer(9))));
     return 0;
 }
 
@@ -391,6 +447,7 @@ const Route kRoutes[] = {
     {"cublas_gemm_int8", cublas_gemm_int8, 5, 0},
     {"dequantize_int8_linear", dequantize_int8_linear, 7, 0},
     {"int8_linear_m1", int8_linear_m1, 16, 11},
+    {"quantize_int8_rowwise_convrot64", quantize_int8_rowwise_convrot64, 10, 0},
 };
 
 }  // namespace

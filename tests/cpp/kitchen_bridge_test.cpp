@@ -35,6 +35,8 @@ using OGemm = void (*)(const int8_t*, const int8_t*, int64_t, int64_t, int64_t, 
 using OEpi = void (*)(const int32_t*, const float*, const float*, int64_t, const void*, void*, int, int64_t, int64_t, int,
                       int);
 using ORes = void (*)(void*, const void*, const void*, int64_t, int, int64_t, int64_t, int);
+using OCrAct = void (*)(const void*, int, int64_t, int64_t, int64_t, int, int, const void*, float, int8_t*, float*,
+                        float*);
 
 static Call call;
 static Text last_error;
@@ -42,6 +44,7 @@ static OQuant o_quant;
 static OGemm o_gemm;
 static OEpi o_epi;
 static ORes o_res;
+static OCrAct o_cract;
 static int failures = 0;
 
 // The crate's KernelArg -> RawArg (native.rs:462-497).
@@ -116,8 +119,9 @@ int main(int argc, char** argv) {
     o_gemm = reinterpret_cast<OGemm>(dlsym(ho, "w8o_gemm_i32"));
     o_epi = reinterpret_cast<OEpi>(dlsym(ho, "w8o_epilogue_kitchen"));
     o_res = reinterpret_cast<ORes>(dlsym(ho, "w8o_residual"));
+    o_cract = reinterpret_cast<OCrAct>(dlsym(ho, "w8o_convrot_quant_act"));
     check(call && last_error && accel && meta, "bridge exports imagine_kitchen_call and imagine_last_*");
-    if (!call || !o_quant || !o_gemm || !o_epi || !o_res) return 1;
+    if (!call || !o_quant || !o_gemm || !o_epi || !o_res || !o_cract) return 1;
 
     at::manual_seed(7);
     const int64_t stream = 0;   // the crate passes torch's current stream; the default one here
@@ -211,6 +215,66 @@ int main(int argc, char** argv) {
                      &result);
             check(rc == 0 && same_bytes(o1b, want1), "int8_linear_m1 (16 arguments) with residual " + dn + " = oracle");
         }
+    }
+
+    // ---- quantize_int8_rowwise_convrot64 with each input activation, and
+    // int8_linear_m1 on the ConvRot route with empty scratch and an activation
+    // (the crate's argument lists: convrot.rs:191-206, cuda_linear.rs:558-582)
+    for (at::ScalarType xdt : {at::kBFloat16, at::kHalf, at::kFloat}) {
+        const std::string xn = xdt == at::kBFloat16 ? "bf16" : xdt == at::kHalf ? "f16" : "f32";
+        const char* names[] = {"none", "gelu_tanh", "swiglu", "rms_norm", "situ"};
+        for (int act = 0; act <= 4; ++act) {
+            const int64_t m = 5, k = 512, width = (act == 2 || act == 4) ? 2 * k : k;
+            const at::Tensor x = (at::randn({m, width}) * 2).to(xdt);
+            const at::Tensor aw = act == 3 ? (1 + 0.3 * at::randn({k})).to(xdt) : at::empty({0}, xdt);
+            at::Tensor q_ref = at::empty({m, k}, at::kChar), s_ref = at::empty({m, 1}, at::kFloat);
+            at::Tensor work = at::empty({k}, at::kFloat);
+            o_cract(x.data_ptr(), code_of(xdt), m, k, 256, /*scale_mode=*/1, act, act == 3 ? aw.data_ptr() : nullptr,
+                    1e-6f, q_ref.data_ptr<int8_t>(), s_ref.data_ptr<float>(), work.data_ptr<float>());
+            const at::Tensor xd = dev(x), awd = dev(aw);
+            at::Tensor q = at::empty({m, k}, at::TensorOptions().dtype(at::kChar).device(at::kCUDA));
+            at::Tensor s = at::empty({m, 1}, at::TensorOptions().dtype(at::kFloat).device(at::kCUDA));
+            int rc = run("quantize_int8_rowwise_convrot64",
+                         {T(xd), T(q), T(s), Int(256), Bool(false), Int(act), Int(0), T(awd), Float(1e-6), Int(stream)},
+                         &result);
+            check(rc == 0 && same_bytes(q, q_ref) && same_bytes(s, s_ref),
+                  std::string("quantize_int8_rowwise_convrot64 ") + names[act] + " " + xn + " = oracle");
+
+            // M = 1 through int8_linear_m1, scratch tensors empty as the crate sends them
+            const int64_t n = 384;
+            const at::Tensor w = at::randint(-127, 128, {n, k}, at::kChar);
+            const at::Tensor ws = at::rand({n}) * 9e-3 + 1e-3;
+            const at::Tensor bias = (at::randn({n}) * 0.02).to(at::kBFloat16);
+            Ref r1;
+            r1.q = q_ref.slice(0, 0, 1).contiguous();
+            r1.xs = s_ref.slice(0, 0, 1).contiguous();
+            r1.acc = at::empty({1, n}, at::kInt);
+            o_gemm(r1.q.data_ptr<int8_t>(), w.data_ptr<int8_t>(), 1, n, k, r1.acc.data_ptr<int32_t>());
+            const at::Tensor want = oracle_epilogue(r1, ws, &bias, at::kBFloat16);
+            const at::Tensor x1d = dev(x.slice(0, 0, 1).contiguous()), wd = dev(w), wsd = dev(ws), bd = dev(bias);
+            const at::Tensor eq = at::empty({0}, at::TensorOptions().dtype(at::kChar).device(at::kCUDA));
+            const at::Tensor es = at::empty({0}, at::TensorOptions().dtype(at::kFloat).device(at::kCUDA));
+            at::Tensor o = at::empty({1, n}, at::TensorOptions().dtype(at::kBFloat16).device(at::kCUDA));
+            rc = run("int8_linear_m1",
+                     {T(x1d), T(eq), T(es), T(wd), T(wsd), T(bd), T(o), Int(2), Bool(true), Int(256), Int(act), T(awd),
+                      Float(1e-6), Int(stream), None(), None()},
+                     &result);
+            check(rc == 0 && same_bytes(o, want), std::string("int8_linear_m1 ConvRot ") + names[act] + " " + xn +
+                                                      " (empty scratch) = oracle" + (rc ? ": " + std::string(last_error()) : ""));
+        }
+        // Kitchen's texts for a bad output width and a missing norm weight
+        const at::Tensor x = at::zeros({4, 512}, at::TensorOptions().dtype(xdt).device(at::kCUDA));
+        at::Tensor q = at::empty({4, 512}, at::TensorOptions().dtype(at::kChar).device(at::kCUDA));
+        at::Tensor s = at::empty({4, 1}, at::TensorOptions().dtype(at::kFloat).device(at::kCUDA));
+        const at::Tensor none = at::empty({0}, at::TensorOptions().dtype(xdt).device(at::kCUDA));
+        int rc = run("quantize_int8_rowwise_convrot64",
+                     {T(x), T(q), T(s), Int(256), Bool(false), Int(2), Int(0), T(none), Float(0.0), Int(stream)}, &result);
+        check(rc == -1 && std::string(last_error()) == "INT8 rowwise convrot64 output shape mismatch",
+              "convrot64 swiglu width text " + xn);
+        rc = run("quantize_int8_rowwise_convrot64",
+                 {T(x), T(q), T(s), Int(256), Bool(false), Int(3), Int(0), T(none), Float(0.0), Int(stream)}, &result);
+        check(rc == -1 && std::string(last_error()) == "INT8 rowwise convrot64 rms_norm weight must have K elements",
+              "convrot64 rms_norm weight text " + xn);
     }
 
     // ---- errors: codes and texts
