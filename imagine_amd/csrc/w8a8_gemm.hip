@@ -14,7 +14,7 @@ bool gemm_mfma_supported(const void* a, size_t a_elem, const int8_t* w, int64_t 
 }
 
 // Compute units of the current device (cached per device).
-static int device_cus() {
+int device_cus() {
     static int cus[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;

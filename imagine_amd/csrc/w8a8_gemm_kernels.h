@@ -431,124 +431,172 @@ __device__ __forceinline__ int out_swz(int row) {
     return row & (kPeriod - 1);
 }
 
-// Dequantize the block's accumulators into the LDS ring as a BM x BN tile of
-// 16-bit values, then write it out row by row, 16 bytes per lane (N % 8 == 0,
-// 16-byte aligned out).  Same values as store_tiles.
-// MODE 2 adds the residual in the write-out pass, where the residual row and
-// the scales are read as 16-byte chunks (resid and a per-channel rscale
-// 16-byte aligned, which the caller checks).
-template <int ODT, int MODE, bool GELU, class C, class Side>
-__device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::TM], int8_t* lds,
-                                                   int lane, int t, int m_base, int n_base,
-                                                   int wave_m, int wave_n, int M, int N,
-                                                   const float* __restrict__ xs,
-                                                   const float* __restrict__ ws, int64_t ws_size,
-                                                   const void* __restrict__ bias, const Residual& res,
-                                                   void* __restrict__ out,
-                                                   const float (&side_v)[Side::kIters],
-                                                   const float (&side_b)[Side::kIters]) {
+// Block barrier for LDS data only: this wave's LDS accesses have completed
+// (lgkmcnt(0)), then s_barrier.  Unlike __syncthreads(), whose release fence
+// also waits for outstanding LDS-DMA tile loads (vmcnt(0)), it lets loads
+// issued into another LDS region stay in flight.  The empty asm statements
+// keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // gfx9: vmcnt 63, expcnt 7, lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// Epilogue of 16-bit outputs through an LDS staging area, in PASSES passes
+// of BM / PASSES rows.  In pass p the waves holding those rows (waves
+// [p * W / PASSES, (p + 1) * W / PASSES), W the block's waves) dequantize
+// their accumulators and write them as rows of BN 16-bit values, the 16-byte
+// chunk index XOR-swizzled by the row; then every thread reads whole rows
+// back, 16 bytes per lane, and stores them, so each output line is written
+// whole (N % 8 == 0, out 16-byte aligned).  For MFMA tile (i, j) a lane holds
+// token m = wave_m + 32 j + lane % 32 and channels n = wave_n + 32 i + 8 g +
+// 4 (lane / 32) + {0..3} in acc[i][j][4g .. 4g+3]; the values equal
+// store_tiles'.  Scales come from the side area when it is in use (written
+// and made visible by the caller), else from global memory.
+// before_store() runs once, after the first pass is staged and before its
+// first global store (a wait for loads the caller issued earlier).  MODE 2
+// adds the residual in the write-out, reading the residual row and the
+// scales as 16-byte chunks (resid and a per-channel rscale 16-byte aligned,
+// which the caller checks).  Starts with the staging area free; ends with a
+// barrier after the last read of it (LDS only: tile loads the caller has in
+// flight into other LDS stay in flight).
+template <int ODT, int MODE, bool GELU, class C, class Side, int PASSES, class Hook>
+__device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::TM], const int8_t* lds,
+                                                   int8_t* stage, int lane, int t, int wave, int m_base,
+                                                   int n_base, int wave_m, int wave_n, int M, int N,
+                                                   const float* __restrict__ xs, const float* __restrict__ ws,
+                                                   int64_t ws_size, const void* __restrict__ bias,
+                                                   const Residual& res, void* __restrict__ out,
+                                                   Hook before_store) {
     constexpr int BN = C::BN, BM = C::BM, TN = C::TN, TM = C::TM;
     constexpr int kRowBytes = BN * 2;
     constexpr int kChunks = BN / 8;   // 16-byte chunks per staged row
+    constexpr int kRows = BM / PASSES;
+    constexpr int kWavesPerPass = C::kWaves / PASSES;
+    static_assert((BM / C::WM) % PASSES == 0, "each pass holds whole wave rows");
+    static_assert(kRows * kChunks % C::kThreads == 0, "whole write-out passes over the block");
     using OS = typename DType<ODT>::storage;
-    const int lane_m = lane % 32, half = lane / 32;
-    float* const sv = reinterpret_cast<float*>(lds + C::kLds);   // [BM xs | BN ws]
-    float* const sb = sv + BM + BN;                               // [BN bias]
-    float xsv[TM];
-    if constexpr (Side::kUse) {
-        static_for<0, Side::kIters>([&](auto it) {
-            const int idx = t + it * C::kThreads;
-            if (idx < BM + BN) {
-                sv[idx] = side_v[it];
-                if (idx >= BM) sb[idx - BM] = side_b[it];
-            }
-        });
-    } else {
-        static_for<0, TM>([&](auto j) {
-            const int m = m_base + wave_m + j * 32 + lane_m;
-            xsv[j] = xs[m < M ? m : M - 1];
-        });
-    }
-    __syncthreads();  // every wave has finished reading the last K tile (and the side area is written)
-    if constexpr (Side::kUse) {
-        static_for<0, TM>([&](auto j) { xsv[j] = sv[wave_m + j * 32 + lane_m]; });
-    }
-    static_for<0, TN>([&](auto i) {
-        static_for<0, 4>([&](auto g) {
-            const int chunk = (wave_n + i * 32 + 8 * g) / 8;
-            const int nl = wave_n + i * 32 + 8 * g + 4 * half;
-            const int n0 = n_base + nl;
-            float wsv[4], bv[4];
-            if constexpr (Side::kUse) {
-                const float4 w4 = *reinterpret_cast<const float4*>(sv + BM + nl);
-                const float4 b4 = *reinterpret_cast<const float4*>(sb + nl);
-                wsv[0] = w4.x; wsv[1] = w4.y; wsv[2] = w4.z; wsv[3] = w4.w;
-                bv[0] = b4.x; bv[1] = b4.y; bv[2] = b4.z; bv[3] = b4.w;
-            } else {
-                static_for<0, 4>([&](auto e) {
-                    const int n = n0 + e < N ? n0 + e : N - 1;
-                    wsv[e] = ws[ws_size == 1 ? 0 : n];
-                    bv[e] = bias ? DType<ODT>::load(static_cast<const OS*>(bias)[n]) : 0.0f;
-                });
-            }
+    // Lane-derived addresses are recomputed here from values the compiler
+    // cannot see through, so that in the persistent kernel they are not
+    // hoisted out of the tile loop and kept in registers across the K loop.
+    int ln = lane, tv = t;
+    asm volatile("" : "+v"(ln), "+v"(tv));
+    const int lane_m = ln % 32, half = ln / 32;
+    const float* const sv = reinterpret_cast<const float*>(lds + C::kLds);   // [BM xs | BN ws]
+    const float* const sb = sv + BM + BN;                                      // [BN bias]
+    static_for<0, PASSES>([&](auto p_) {
+        constexpr int p = decltype(p_)::value;
+        if (wave / kWavesPerPass == p) {   // wave-uniform
+            float xsv[TM];
             static_for<0, TM>([&](auto j) {
-                const int ml = wave_m + j * 32 + lane_m;
-                uint2 p;
-                if constexpr (GELU && ODT == W8A8_BF16) {
-                    // round the pre-activations in pairs, then GELU in pairs
-                    float v[4];
-                    static_for<0, 4>([&](auto e) {
-                        v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], false);
-                    });
-                    p.x = gelu_bf16x2(pack2_bf16(v[0], v[1]));
-                    p.y = gelu_bf16x2(pack2_bf16(v[2], v[3]));
+                if constexpr (Side::kUse) {
+                    xsv[j] = sv[wave_m + j * 32 + lane_m];
                 } else {
-                    float v[4];
-                    static_for<0, 4>([&](auto e) {
-                        v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
-                    });
-                    p.x = DType<ODT>::store2(v[0], v[1]);
-                    p.y = DType<ODT>::store2(v[2], v[3]);
+                    const int m = m_base + wave_m + j * 32 + lane_m;
+                    xsv[j] = xs[m < M ? m : M - 1];
                 }
-                *reinterpret_cast<uint2*>(lds + ml * kRowBytes + (chunk ^ out_swz<BN>(ml)) * 16 + half * 8) = p;
             });
-        });
-    });
-    __syncthreads();
-    constexpr int kTotal = BM * kChunks;
-    static_assert(kTotal % C::kThreads == 0, "whole passes over the block");
-#pragma unroll 4
-    for (int pass = 0; pass < kTotal / C::kThreads; ++pass) {
-        const int idx = pass * C::kThreads + t;
-        const int r = idx / kChunks, c = idx % kChunks;
-        const int m = m_base + r, n = n_base + c * 8;
-        uint4 v = *reinterpret_cast<const uint4*>(lds + r * kRowBytes + (c ^ out_swz<BN>(r)) * 16);
-        if (m < M && n < N) {
-            if constexpr (MODE == 2) {
-                const uint4 rv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.resid) +
-                                                                 static_cast<int64_t>(m) * N + n);
-                uint4 sv;
-                if (res.rs_size == 1) {
-                    const uint32_t s1 = static_cast<const OS*>(res.rscale)[0];
-                    sv.x = sv.y = sv.z = sv.w = s1 | (s1 << 16);
-                } else {
-                    sv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.rscale) + n);
-                }
-                auto lo = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w & 0xffffu)); };
-                auto hi = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w >> 16)); };
-                auto fuse = [&](uint32_t lin, uint32_t s, uint32_t rr) {
-                    return DType<ODT>::store2(fmaf(lo(lin), lo(s), lo(rr)), fmaf(hi(lin), hi(s), hi(rr)));
-                };
-                v.x = fuse(v.x, sv.x, rv.x);
-                v.y = fuse(v.y, sv.y, rv.y);
-                v.z = fuse(v.z, sv.z, rv.z);
-                v.w = fuse(v.w, sv.w, rv.w);
-            }
-            *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
+            static_for<0, TN>([&](auto i) {
+                static_for<0, 4>([&](auto g) {
+                    const int chunk = (wave_n + i * 32 + 8 * g) / 8;
+                    const int nl = wave_n + i * 32 + 8 * g + 4 * half;
+                    const int n0 = n_base + nl;
+                    float wsv[4], bv[4];
+                    if constexpr (Side::kUse) {
+                        const float4 w4 = *reinterpret_cast<const float4*>(sv + BM + nl);
+                        const float4 b4 = *reinterpret_cast<const float4*>(sb + nl);
+                        wsv[0] = w4.x; wsv[1] = w4.y; wsv[2] = w4.z; wsv[3] = w4.w;
+                        bv[0] = b4.x; bv[1] = b4.y; bv[2] = b4.z; bv[3] = b4.w;
+                    } else {
+                        static_for<0, 4>([&](auto e) {
+                            const int n = n0 + e < N ? n0 + e : N - 1;
+                            wsv[e] = ws[ws_size == 1 ? 0 : n];
+                            bv[e] = bias ? DType<ODT>::load(static_cast<const OS*>(bias)[n]) : 0.0f;
+                        });
+                    }
+                    static_for<0, TM>([&](auto j) {
+                        float v[4];
+                        uint2 pk;
+                        if constexpr (GELU && ODT == W8A8_BF16) {
+                            // round the pre-activations in pairs, then GELU in pairs
+                            static_for<0, 4>([&](auto e) {
+                                v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], false);
+                            });
+                            pk.x = gelu_bf16x2(pack2_bf16(v[0], v[1]));
+                            pk.y = gelu_bf16x2(pack2_bf16(v[2], v[3]));
+                        } else {
+                            static_for<0, 4>([&](auto e) {
+                                v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
+                            });
+                            pk.x = DType<ODT>::store2(v[0], v[1]);
+                            pk.y = DType<ODT>::store2(v[2], v[3]);
+                        }
+                        const int ml = wave_m + j * 32 + lane_m - p * kRows;
+                        *reinterpret_cast<uint2*>(stage + ml * kRowBytes + (chunk ^ out_swz<BN>(ml)) * 16 + half * 8) =
+                            pk;
+                    });
+                });
+            });
         }
-    }
+        lds_barrier();
+        if constexpr (p == 0) before_store();
+#pragma unroll 4
+        for (int pass = 0; pass < kRows * kChunks / C::kThreads; ++pass) {
+            const int idx = pass * C::kThreads + tv;
+            const int r = idx / kChunks, c = idx % kChunks;
+            const int m = m_base + p * kRows + r, n = n_base + c * 8;
+            uint4 v = *reinterpret_cast<const uint4*>(stage + r * kRowBytes + (c ^ out_swz<BN>(r)) * 16);
+            if (m < M && n < N) {
+                if constexpr (MODE == 2) {
+                    const uint4 rv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.resid) +
+                                                                     static_cast<int64_t>(m) * N + n);
+                    uint4 sv4;
+                    if (res.rs_size == 1) {
+                        const uint32_t s1 = static_cast<const OS*>(res.rscale)[0];
+                        sv4.x = sv4.y = sv4.z = sv4.w = s1 | (s1 << 16);
+                    } else {
+                        sv4 = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.rscale) + n);
+                    }
+                    auto lo = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w & 0xffffu)); };
+                    auto hi = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w >> 16)); };
+                    auto fuse = [&](uint32_t lin, uint32_t s, uint32_t rr) {
+                        return DType<ODT>::store2(fmaf(lo(lin), lo(s), lo(rr)), fmaf(hi(lin), hi(s), hi(rr)));
+                    };
+                    v.x = fuse(v.x, sv4.x, rv.x);
+                    v.y = fuse(v.y, sv4.y, rv.y);
+                    v.z = fuse(v.z, sv4.z, rv.z);
+                    v.w = fuse(v.w, sv4.w, rv.w);
+                }
+                *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
+            }
+        }
+        lds_barrier();
+    });
 }
 
+// Epilogue plan of a DMA configuration for an output mode: kStaged = 16-bit
+// outputs staged through LDS for whole-line stores; kPersist = the kernel
+// loops over output tiles (grid = min(tiles, CUs)) and overlaps each
+// epilogue with the next tile's first loads, which needs a 2-stage ring whose
+// stage holds half of the output tile.
+template <class C, int ODT, int MODE>
+struct DmaPlan {
+    static constexpr bool kStaged = MODE != 1 && ODT != W8A8_F32 && C::kStageOut;
+    static constexpr bool kPersist =
+        kStaged && C::STAGES == 2 && C::BN * C::BM <= C::kTileBytes && (C::BM / C::WM) % 2 == 0;
+};
+
+// Persistent INT8 GEMM over LDS-DMA K tiles.  Block b takes output tiles b,
+// b + G, b + 2G, ... (G = gridDim.x; with G = the tile count each block takes
+// one).  Per tile: the K loop below, then the epilogue.  With a 2-stage ring
+// whose stage holds half of the 16-bit output tile, the epilogue overlaps the
+// next tile's start: once every wave has left the K loop, K tile 0 of the
+// next output tile is loaded into the stage the last K tile did not use, the
+// accumulators are dequantized in registers meanwhile, the output is staged
+// in two passes through the other stage and stored, and K tile 1 of the next
+// tile is issued into it; the stores then drain under the next K loop.
 template <int ODT, int MODE, bool GELU, class C>
 __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     const int8_t* __restrict__ q, const int8_t* __restrict__ w, const float* __restrict__ xs,
@@ -559,79 +607,70 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     constexpr int kTileBytes = C::kTileBytes, kLoadsPerThread = C::kLoadsPerThread;
     constexpr int kWWaveLoads = C::kWWaveLoads;
     using Side = SideArea<C, ODT, MODE>;
+    constexpr bool kStaged = DmaPlan<C, ODT, MODE>::kStaged;
+    constexpr bool kPersist = DmaPlan<C, ODT, MODE>::kPersist;
     __shared__ __attribute__((aligned(1024))) int8_t lds[C::kLds + Side::kBytes];
 
-    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-    const TileCoord tc = tile_of_block(blockIdx.x, tiles_m, tiles_n, group_m);
-    const int m_base = tc.tm * BM, n_base = tc.tn * BN;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
     // The wave index is uniform across the wave: in an SGPR, so operand choice,
     // buffer resources and LDS destinations of the tile loads stay scalar.
     const int t = threadIdx.x, lane = t % kWave, wave = __builtin_amdgcn_readfirstlane(t / kWave);
-
-    // Epilogue scales of this block (side area): value idx < BM is xs of row
-    // m_base + idx, else ws and bias of channel n_base + idx - BM (clamped to
-    // the last row / channel, as the direct epilogue clamps them).
-    float side_v[Side::kIters], side_b[Side::kIters];
-    if constexpr (Side::kUse) {
-        using OS = typename DType<ODT>::storage;
-        static_for<0, Side::kIters>([&](auto it) {
-            const int idx = t + it * C::kThreads;
-            side_v[it] = 0.0f;
-            side_b[it] = 0.0f;
-            if (idx < BM) {
-                const int m = m_base + idx;
-                side_v[it] = xs[m < M ? m : M - 1];
-            } else if (idx < BM + BN) {
-                int n = n_base + idx - BM;
-                n = n < N ? n : N - 1;
-                side_v[it] = ws[ws_size == 1 ? 0 : n];
-                if (bias) side_b[it] = DType<ODT>::load(static_cast<const OS*>(bias)[n]);
-            }
-        });
-    }
     const int wave_n = (wave % (BN / WN)) * WN;
     const int wave_m = (wave / (BN / WN)) * WM;
     const int KT = K / BK;                                 // K % BK == 0 (host checks)
+    bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+    if constexpr (MODE == 2)
+        vec_ok = vec_ok && (reinterpret_cast<uintptr_t>(res.resid) % 16) == 0 &&
+                 (res.rs_size == 1 || (reinterpret_cast<uintptr_t>(res.rscale) % 16) == 0);
+
+    int tile = blockIdx.x;
+    TileCoord tc = tile_of_block(tile, tiles_m, tiles_n, group_m);
+    int m_base = tc.tm * BM, n_base = tc.tn * BN;
 
     // Source of each wave-load this lane takes part in: wave-load L (global
     // index j * kWaves + wave, L < kWaveLoads) fills LDS chunks [64 L, 64 L + 64)
     // of the stage; chunk p holds row p / CPR, logical chunk (p % CPR) ^ swz(row).
     // Byte offsets into a buffer resource per operand (the K offset of a
     // tile goes in the scalar offset).  Each operand's resource is based at
-    // the block's first tile row, so offsets stay below BN * K (or BM * K)
-    // bytes whatever the operand's size (the host checks that bound).
-    const int8_t* const wb = w + static_cast<int64_t>(n_base) * K;
-    const int8_t* const qb = q + static_cast<int64_t>(m_base) * K;
-    uint32_t voff[kLoadsPerThread];
-#pragma unroll
-    for (int j = 0; j < kLoadsPerThread; ++j) {
+    // the loaded tile's first row, so offsets stay below BN * K (or BM * K)
+    // bytes whatever the operand's size (the host checks that bound).  The
+    // offsets are recomputed per load (a few VALU operations) rather than
+    // kept in registers across the loop.
+    int ld_mb = m_base, ld_nb = n_base;   // the output tile whose K tiles issue() loads
+    auto set_tile = [&](int mb, int nb) {
+        ld_mb = mb;
+        ld_nb = nb;
+    };
+    auto voff_of = [&](int j) -> uint32_t {
         const int L = j * C::kWaves + wave < C::kWaveLoads ? j * C::kWaves + wave : C::kWaveLoads - 1;
         const bool is_w = L < kWWaveLoads;
         const int p = (is_w ? L : L - kWWaveLoads) * 64 + lane;
         const int r = p / CPR;
         const int c = (p % CPR) ^ swz<BK>(r);
-        const int base = is_w ? n_base : m_base;
+        const int base = is_w ? ld_nb : ld_mb;
         const int lim = is_w ? N : M;
         const int row = base + r < lim ? r : lim - 1 - base;   // clamped to the last row, relative
-        voff[j] = static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + c * 16;
-    }
-    auto issue = [&](int kt, int stage) {
+        return static_cast<uint32_t>(row) * static_cast<uint32_t>(K) + c * 16;
+    };
+    // Loads [j0, j1) of this lane's share of K tile kt into ring stage `stage`.
+    auto issue = [&](int kt, int stage, int j0, int j1) {
         const int k0 = kt * BK;
+        const int8_t* const wb = w + static_cast<int64_t>(ld_nb) * K;
+        const int8_t* const qb = q + static_cast<int64_t>(ld_mb) * K;
 #pragma unroll
         for (int j = 0; j < kLoadsPerThread; ++j) {
+            if (j < j0 || j >= j1) continue;
             const int L = j * C::kWaves + wave;
             if (C::kWavesWithMore != 0 && L >= C::kWaveLoads) break;   // wave-uniform
             int8_t* dst = lds + stage * kTileBytes + L * 1024;
             buffer_load_lds16(L < kWWaveLoads ? static_cast<const void*>(wb) : static_cast<const void*>(qb), dst,
-                              voff[j], k0);
+                              voff_of(j), k0);
         }
     };
-
-    v16i acc[TN][TM];
-#pragma unroll
-    for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = v16i{};
+    // Half of a K tile's loads are issued right after the barrier that frees
+    // its stage, the other half one substep later, so the loads of the eight
+    // waves do not all queue at the address unit at once.
+    constexpr int kFirst = kLoadsPerThread / 2 > 0 ? kLoadsPerThread / 2 : kLoadsPerThread;
 
     const int fl = swz<BK>(lane % 32);
     int rd[KS];
@@ -639,10 +678,6 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     for (int ks = 0; ks < KS; ++ks) rd[ks] = (((2 * ks + lane / 32) ^ fl) * 16);
     const int wrow = (wave_n + lane % 32) * BK;
     const int xrow = (BN + wave_m + lane % 32) * BK;
-
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-        if (s < KT) issue(s, s);
 
     // Fragments of one k32 substep: TN weight fragments, TM activation fragments.
     auto read_frags = [&](int stage, int ks, v4i (&a)[TN], v4i (&b)[TM]) {
@@ -654,6 +689,7 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
         for (int j = 0; j < TM; ++j)
             b[j] = *reinterpret_cast<const v4i*>(base + xrow + j * 32 * BK);
     };
+    v16i acc[TN][TM];
     auto mfmas = [&](const v4i (&a)[TN], const v4i (&b)[TM]) {
 #pragma unroll
         for (int i = 0; i < TN; ++i)
@@ -685,78 +721,180 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
             }
         });
     };
-
-    v4i fa[2][TN], fb[2][TM];   // two fragment sets, alternating by substep parity
-    if (KT > 0) {
-        wait_tile(KT - 1 < STAGES - 2 ? KT - 1 : STAGES - 2);
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-        if (STAGES - 1 < KT) issue(STAGES - 1, STAGES - 1);
-        read_frags(0, 0, fa[0], fb[0]);
-    }
-    // One K tile.  The fragment set of substep ks is fa/fb[(ks + P) & 1]; with an
-    // odd number of substeps per tile the parity flips from tile to tile, so
-    // tiles are then processed in pairs (P = 0, 1) to keep every register index
-    // a compile-time constant.
-    auto tile = [&](int kt, int stage, int next, auto par) {
-        constexpr int P = decltype(par)::value;
-        static_for<0, KS>([&](auto ks_) {
-            constexpr int ks = decltype(ks_)::value;
-            constexpr int cur = (ks + P) & 1;
-            if constexpr (ks + 1 < KS) {
-                read_frags(stage, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
-            } else {
-                if (kt + 1 < KT) {
-                    // tiles issued so far: up to min(KT - 1, kt + STAGES - 1)
-                    const int last = KT - 1 < kt + STAGES - 1 ? KT - 1 : kt + STAGES - 1;
-                    wait_tile(last - (kt + 1));
-                    __builtin_amdgcn_s_barrier();
-                    __builtin_amdgcn_sched_barrier(0);
-                    if (kt + STAGES < KT) issue(kt + STAGES, stage);
-                }
-                // first fragments of the next tile (after the last tile: an
-                // unused in-bounds read, which keeps this one basic block)
-                read_frags(next, 0, fa[cur ^ 1], fb[cur ^ 1]);
-            }
-            // The single MFMA block of the substep: one copy only, so the
-            // accumulators stay in AGPRs.
-            mfmas(fa[cur], fb[cur]);
-            interleave();
-            __builtin_amdgcn_sched_barrier(0);
-        });
-    };
     auto next_stage = [](int st) { return st + 1 == STAGES ? 0 : st + 1; };
-    int stage = 0;
-    if constexpr (KS % 2 == 0) {
-        for (int kt = 0; kt < KT; ++kt) {
-            const int next = next_stage(stage);
-            tile(kt, stage, next, std::integral_constant<int, 0>{});
-            stage = next;
-        }
-    } else {
-        int kt = 0;
-        for (; kt + 1 < KT; kt += 2) {
-            const int s1 = next_stage(stage), s2 = next_stage(s1);
-            tile(kt, stage, s1, std::integral_constant<int, 0>{});
-            tile(kt + 1, s1, s2, std::integral_constant<int, 1>{});
-            stage = s2;
-        }
-        if (kt < KT) tile(kt, stage, next_stage(stage), std::integral_constant<int, 0>{});
-    }
 
-    if constexpr (MODE != 1 && ODT != W8A8_F32 && C::kStageOut) {
-        bool vec_ok = (N % 8) == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0;
-        if constexpr (MODE == 2)
-            vec_ok = vec_ok && (reinterpret_cast<uintptr_t>(res.resid) % 16) == 0 &&
-                     (res.rs_size == 1 || (reinterpret_cast<uintptr_t>(res.rscale) % 16) == 0);
-        if (vec_ok) {
-            store_tiles_staged<ODT, MODE, GELU, C, Side>(acc, lds, lane, t, m_base, n_base, wave_m, wave_n, M,
-                                                         N, xs, ws, ws_size, bias, res, out, side_v, side_b);
-            return;
+    int s0 = 0;           // ring stage of the current tile's K tile 0
+    bool primed = false;  // K tile 0 landed (and waited for) and K tile 1 issued by the previous epilogue
+    for (;;) {
+        // Epilogue scales of this tile (side area): value idx < BM is xs of row
+        // m_base + idx, else ws and bias of channel n_base + idx - BM (clamped to
+        // the last row / channel, as the direct epilogue clamps them).  Their
+        // load latency hides under the K loop.
+        float side_v[Side::kIters], side_b[Side::kIters];
+        if constexpr (Side::kUse) {
+            using OS = typename DType<ODT>::storage;
+            static_for<0, Side::kIters>([&](auto it) {
+                const int idx = t + it * C::kThreads;
+                side_v[it] = 0.0f;
+                side_b[it] = 0.0f;
+                if (idx < BM) {
+                    const int m = m_base + idx;
+                    side_v[it] = xs[m < M ? m : M - 1];
+                } else if (idx < BM + BN) {
+                    int n = n_base + idx - BM;
+                    n = n < N ? n : N - 1;
+                    side_v[it] = ws[ws_size == 1 ? 0 : n];
+                    if (bias) side_b[it] = DType<ODT>::load(static_cast<const OS*>(bias)[n]);
+                }
+            });
         }
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) acc[i][j] = v16i{};
+
+        v4i fa[2][TN], fb[2][TM];   // two fragment sets, alternating by substep parity
+        if (!primed) {
+            int st = s0;
+#pragma unroll
+            for (int s = 0; s < STAGES - 1; ++s) {
+                if (s < KT) issue(s, st, 0, kLoadsPerThread);
+                st = next_stage(st);
+            }
+            if (KT > 0) {
+                wait_tile(KT - 1 < STAGES - 2 ? KT - 1 : STAGES - 2);
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                if (STAGES - 1 < KT) issue(STAGES - 1, st, 0, kLoadsPerThread);
+            }
+        }
+        if (KT > 0) read_frags(s0, 0, fa[0], fb[0]);
+        // One K tile.  The fragment set of substep ks is fa/fb[(ks + P) & 1]; with an
+        // odd number of substeps per tile the parity flips from tile to tile, so
+        // tiles are then processed in pairs (P = 0, 1) to keep every register index
+        // a compile-time constant.  Synchronisation: one raw s_barrier per K tile,
+        // preceded by s_waitcnt vmcnt(loads of later tiles) lgkmcnt(0): the wave's
+        // own DMA for the tile about to be read has landed and its reads of the
+        // tile just consumed have completed, so after the barrier every wave may
+        // read the new tile and the consumed stage may be refilled.  The barrier
+        // is crossed before the last k32 substep of a tile, so the LDS latency of
+        // the next tile's first fragments hides under that substep's MFMAs.
+        auto ktile = [&](int kt, int stage, int next, auto par) {
+            constexpr int P = decltype(par)::value;
+            static_for<0, KS>([&](auto ks_) {
+                constexpr int ks = decltype(ks_)::value;
+                constexpr int cur = (ks + P) & 1;
+                if constexpr (ks == 0 && kFirst < kLoadsPerThread) {
+                    // the second half of the loads issued at the previous barrier
+                    if (kt >= 1 && kt - 1 + STAGES < KT)
+                        issue(kt - 1 + STAGES, stage == 0 ? STAGES - 1 : stage - 1, kFirst, kLoadsPerThread);
+                }
+                if constexpr (ks + 1 < KS) {
+                    read_frags(stage, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+                } else {
+                    if (kt + 1 < KT) {
+                        // tiles issued so far: up to min(KT - 1, kt + STAGES - 1)
+                        const int last = KT - 1 < kt + STAGES - 1 ? KT - 1 : kt + STAGES - 1;
+                        wait_tile(last - (kt + 1));
+                        __builtin_amdgcn_s_barrier();
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (kt + STAGES < KT) issue(kt + STAGES, stage, 0, kFirst);
+                    }
+                    // first fragments of the next tile (after the last tile: an
+                    // unused in-bounds read, which keeps this one basic block)
+                    read_frags(next, 0, fa[cur ^ 1], fb[cur ^ 1]);
+                }
+                // The single MFMA block of the substep: one copy only, so the
+                // accumulators stay in registers.
+                mfmas(fa[cur], fb[cur]);
+                interleave();
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        };
+        int stage = s0;
+        if constexpr (KS % 2 == 0) {
+            for (int kt = 0; kt < KT; ++kt) {
+                const int nx = next_stage(stage);
+                ktile(kt, stage, nx, std::integral_constant<int, 0>{});
+                stage = nx;
+            }
+        } else {
+            int kt = 0;
+            for (; kt + 1 < KT; kt += 2) {
+                const int s1 = next_stage(stage), s2 = next_stage(s1);
+                ktile(kt, stage, s1, std::integral_constant<int, 0>{});
+                ktile(kt + 1, s1, s2, std::integral_constant<int, 1>{});
+                stage = s2;
+            }
+            if (kt < KT) {
+                const int s1 = next_stage(stage);
+                ktile(kt, stage, s1, std::integral_constant<int, 0>{});
+                stage = s1;
+            }
+        }
+        // `stage` is now the one after the last K tile's: for a 2-stage ring the
+        // stage the last K tile did not use.
+        const int s_last = stage == 0 ? STAGES - 1 : stage - 1;
+
+        const int next = tile + static_cast<int>(gridDim.x);
+        const bool has_next = next < tiles;
+        bool stored = false;
+        if constexpr (kStaged) {
+            if (vec_ok) {
+                if constexpr (Side::kUse) {
+                    float* const sv = reinterpret_cast<float*>(lds + C::kLds);
+                    float* const sb = sv + BM + BN;
+                    static_for<0, Side::kIters>([&](auto it) {
+                        const int idx = t + it * C::kThreads;
+                        if (idx < BM + BN) {
+                            sv[idx] = side_v[it];
+                            if (idx >= BM) sb[idx - BM] = side_b[it];
+                        }
+                    });
+                }
+                __syncthreads();   // no wave reads the ring any more; the side area is written
+                if constexpr (kPersist) {
+                    if (has_next && KT > 0) {
+                        const TileCoord nc = tile_of_block(next, tiles_m, tiles_n, group_m);
+                        set_tile(nc.tm * BM, nc.tn * BN);
+                        issue(0, stage, 0, kLoadsPerThread);   // K tile 0 of the next output tile
+                    }
+                    // stage through the last K tile's stage in two passes; K tile 0 of
+                    // the next tile is waited for before the first store, so no store
+                    // is ever pending under a partial vmcnt wait for tile loads
+                    store_tiles_staged<ODT, MODE, GELU, C, Side, 2>(
+                        acc, lds, lds + s_last * kTileBytes, lane, t, wave, m_base, n_base, wave_m, wave_n, M, N, xs,
+                        ws, ws_size, bias, res, out, [&]() { wait_vm_lgkm0<0>(); });
+                    if (!has_next) return;
+                    if (1 < KT) issue(1, s_last, 0, kLoadsPerThread);
+                    tile = next;
+                    tc = tile_of_block(tile, tiles_m, tiles_n, group_m);
+                    m_base = tc.tm * BM;
+                    n_base = tc.tn * BN;
+                    s0 = stage;
+                    primed = true;
+                    continue;
+                } else {
+                    store_tiles_staged<ODT, MODE, GELU, C, Side, 1>(acc, lds, lds, lane, t, wave, m_base, n_base,
+                                                                    wave_m, wave_n, M, N, xs, ws, ws_size, bias,
+                                                                    res, out, []() {});
+                }
+                stored = true;
+            }
+        }
+        if (!stored)
+            store_tiles<ODT, MODE, GELU, TN, TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
+                                                 ws_size, bias, res, out);
+        if (!kPersist || !has_next) return;
+        __syncthreads();   // the LDS is free for the next tile's loads
+        tile = next;
+        tc = tile_of_block(tile, tiles_m, tiles_n, group_m);
+        m_base = tc.tm * BM;
+        n_base = tc.tn * BN;
+        set_tile(m_base, n_base);
+        s0 = 0;
+        primed = false;
     }
-    store_tiles<ODT, MODE, GELU, TN, TM>(acc, lane, m_base, n_base, wave_m, wave_n, M, N, xs, ws,
-                                         ws_size, bias, res, out);
 }
 
 // Generic GEMM for shapes the MFMA kernel does not take (K % 16 != 0,

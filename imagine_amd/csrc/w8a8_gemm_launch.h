@@ -40,12 +40,18 @@ using CfgN256M256W8 = DmaCfg<256, 256, 128, 64, 128, 2, 2>;
 using CfgN384M192W8 = DmaCfg<384, 192, 96, 96, 128, 2, 2>;
 using CfgN256M128 = DmaCfg<256, 128, 128, 64, 64, 3, 2>;
 
+// Compute units of the current device (cached per device; w8a8_gemm.hip).
+int device_cus();
+
 template <class C, int ODT, int MODE, bool GELU>
 inline void launch_dma(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                        int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
                        int64_t N, int64_t K, hipStream_t stream) {
     const int tiles = static_cast<int>(((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN));
-    hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C>), dim3(tiles), dim3(C::kThreads), 0, stream, q, w, xs,
+    // one block per CU looping over tiles, or one block per tile
+    const int cus = device_cus();
+    const int grid = DmaPlan<C, ODT, MODE>::kPersist && tiles > cus ? cus : tiles;
+    hipLaunchKernelGGL((gemm_mfma_dma<ODT, MODE, GELU, C>), dim3(grid), dim3(C::kThreads), 0, stream, q, w, xs,
                        ws, ws_size, bias, res, out, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
                        kGroupM);
 }
