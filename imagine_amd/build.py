@@ -97,7 +97,9 @@ def build(verbose=False, extra=()):
         with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
             objs = list(ex.map(compile_one, SOURCES))
         tmp_lib = Path(tmp) / LIB.name
-        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp_lib)]
+        # -z defs: a kernel whose host launch stub the compiler dropped fails here,
+        # not at load time
+        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objs), "-o", str(tmp_lib)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"link failed:\n{r.stderr}")
