@@ -5,13 +5,14 @@
 // adaLN modulation projection, M = 2 rows (conditional + unconditional), a
 // weight-streaming, HBM-bound kernel.
 //
-// Layout of the work: every wave first loads the M activation rows into
-// registers (K <= 64 lanes * XC chunks * 16 B), then walks output channels
-// RPW at a time with a grid stride, streaming each weight row once with
-// 128-bit loads and v_dot4_i32_i8 (sdot4), reducing the per-lane partial dot
-// products with a wave64 butterfly.  Larger K re-reads the activation chunks
-// from L1 instead of holding them.  K % 16 != 0 or unaligned operands take the
-// generic kernel (one wave per channel, byte loads).
+// Layout of the work: each block stages the M activation rows in LDS and every
+// wave copies its chunks into registers (K <= 64 lanes * XC chunks * 16 B),
+// then walks output channels RPW at a time with a grid stride, streaming each
+// weight row once with 128-bit loads (all chunks of a row in flight at once)
+// and v_dot4_i32_i8 (sdot4), reducing the per-lane partial dot products with a
+// wave64 butterfly.  Larger K re-reads the activation chunks from L1 instead
+// of holding them.  K % 16 != 0 or unaligned operands take the generic kernel
+// (one wave per channel, byte loads).
 #include "w8a8_common.h"
 
 namespace w8a8 {
@@ -35,35 +36,61 @@ __device__ __forceinline__ int dot16(const uint4 a, const uint4 b, int acc) {
 }
 
 // XC: activation chunks per lane held in registers (0 = stream them from cache).
+// Launched with kGemvThreads threads per block.
+constexpr int kGemvThreads = 512;
+
 template <int ODT, int MR, int RPW, int XC>
-__global__ __launch_bounds__(256) void gemv_vec(const int8_t* __restrict__ q,
-                                                const int8_t* __restrict__ w,
-                                                const float* __restrict__ xs,
-                                                const float* __restrict__ ws, int64_t ws_size,
-                                                const void* __restrict__ bias, Residual res,
-                                                void* __restrict__ out, int64_t N, int64_t K,
-                                                int gelu) {
+__global__ __launch_bounds__(kGemvThreads) void gemv_vec(const int8_t* __restrict__ q,
+                                                         const int8_t* __restrict__ w,
+                                                         const float* __restrict__ xs,
+                                                         const float* __restrict__ ws, int64_t ws_size,
+                                                         const void* __restrict__ bias, Residual res,
+                                                         void* __restrict__ out, int64_t N, int64_t K,
+                                                         int gelu) {
     const int lane = threadIdx.x % kWave;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * (blockDim.x / kWave);
     const int64_t nchunks = K / 16;
     const uint4* qv = reinterpret_cast<const uint4*>(q);
+    const int64_t stride = nwaves * RPW;
+    int64_t n0 = wave * RPW;
 
+    // Weight chunks of RPW rows: all of them are loaded before the first dot
+    // product, so one memory round trip covers them; lanes past K load chunk 0
+    // again and multiply it by their zero activation chunk.
+    uint4 wv[RPW][XC > 0 ? XC : 1];
+    auto load_rows = [&](int64_t nb) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int64_t n = nb + r < N ? nb + r : N - 1;
+#pragma unroll
+            for (int j = 0; j < (XC > 0 ? XC : 1); ++j) {
+                const int64_t c = lane + j * kWave;
+                wv[r][j] = reinterpret_cast<const uint4*>(w + n * K)[c < nchunks ? c : 0];
+            }
+        }
+    };
+    // XC > 0: the block stages the M activation rows in LDS once (one pass of
+    // 16-byte loads) and every wave takes its chunks from there, instead of
+    // each wave loading them from L2.
     uint4 xr[MR][XC > 0 ? XC : 1];
     if constexpr (XC > 0) {
+        __shared__ uint4 xl[MR * XC * kWave];
+        for (int64_t i = threadIdx.x; i < MR * nchunks; i += blockDim.x) xl[i] = qv[i];
+        __syncthreads();
 #pragma unroll
         for (int m = 0; m < MR; ++m)
 #pragma unroll
             for (int j = 0; j < XC; ++j) {
                 const int64_t c = lane + j * kWave;
-                xr[m][j] = c < nchunks ? qv[m * nchunks + c] : make_uint4(0, 0, 0, 0);
+                xr[m][j] = c < nchunks ? xl[m * nchunks + c] : make_uint4(0, 0, 0, 0);
             }
     }
     float xsc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) xsc[m] = xs[m];
 
-    for (int64_t n0 = wave * RPW; n0 < N; n0 += nwaves * RPW) {
+    for (; n0 < N; n0 += stride) {
         int acc[MR][RPW];
 #pragma unroll
         for (int m = 0; m < MR; ++m)
@@ -71,19 +98,15 @@ __global__ __launch_bounds__(256) void gemv_vec(const int8_t* __restrict__ q,
             for (int r = 0; r < RPW; ++r) acc[m][r] = 0;
 
         if constexpr (XC > 0) {
+            // (a prefetch of the next rows here raises the register count past
+            // 64 and so the occupancy below 8 waves per SIMD: measured slower)
+            load_rows(n0);
 #pragma unroll
-            for (int j = 0; j < XC; ++j) {
-                const int64_t c = lane + j * kWave;
-                if (c < nchunks) {
+            for (int j = 0; j < XC; ++j)
 #pragma unroll
-                    for (int r = 0; r < RPW; ++r) {
-                        const int64_t n = n0 + r < N ? n0 + r : N - 1;
-                        const uint4 wv = reinterpret_cast<const uint4*>(w + n * K)[c];
+                for (int r = 0; r < RPW; ++r)
 #pragma unroll
-                        for (int m = 0; m < MR; ++m) acc[m][r] = dot16(xr[m][j], wv, acc[m][r]);
-                    }
-                }
-            }
+                    for (int m = 0; m < MR; ++m) acc[m][r] = dot16(xr[m][j], wv[r][j], acc[m][r]);
         } else {
             for (int64_t c = lane; c < nchunks; c += kWave) {
                 uint4 xv[MR];
@@ -92,9 +115,9 @@ __global__ __launch_bounds__(256) void gemv_vec(const int8_t* __restrict__ q,
 #pragma unroll
                 for (int r = 0; r < RPW; ++r) {
                     const int64_t n = n0 + r < N ? n0 + r : N - 1;
-                    const uint4 wv = reinterpret_cast<const uint4*>(w + n * K)[c];
+                    const uint4 wc = reinterpret_cast<const uint4*>(w + n * K)[c];
 #pragma unroll
-                    for (int m = 0; m < MR; ++m) acc[m][r] = dot16(xv[m], wv, acc[m][r]);
+                    for (int m = 0; m < MR; ++m) acc[m][r] = dot16(xv[m], wc, acc[m][r]);
                 }
             }
         }
@@ -154,7 +177,7 @@ template <int ODT, int MR, int RPW, int XC>
 static void launch_gemv_vec(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                             int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t N, int64_t K,
                             int gelu, int blocks, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_vec<ODT, MR, RPW, XC>), dim3(blocks), dim3(256), 0, stream, q, w, xs,
+    hipLaunchKernelGGL((gemv_vec<ODT, MR, RPW, XC>), dim3(blocks), dim3(kGemvThreads), 0, stream, q, w, xs,
                        ws, ws_size, bias, res, out, N, K, gelu);
 }
 
@@ -162,11 +185,15 @@ template <int ODT, int MR>
 static void gemv_dispatch_m(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                             int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t N, int64_t K,
                             int gelu, hipStream_t stream) {
-    constexpr int RPW = 2;
-    // Enough waves to keep every CU streaming, never more than one pass of channels.
+    // One channel per wave iteration and 32 waves per CU (8 per SIMD), each
+    // walking its channels with a grid stride: at the adaLN shape (K = 3072,
+    // N = 18432) this measured fastest of 1-9 channels per wave, 256- to
+    // 1024-thread blocks and 4096-18432 waves.
+    constexpr int RPW = 1;
+    constexpr int kWavesPerBlock = kGemvThreads / kWave;
     const int64_t waves_needed = (N + RPW - 1) / RPW;
-    int64_t blocks = (waves_needed + 3) / 4;
-    if (blocks > 2048) blocks = 2048;
+    int64_t blocks = (waves_needed + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (blocks > 8192 / kWavesPerBlock) blocks = 8192 / kWavesPerBlock;
     const int64_t nchunks = K / 16;
     const int b = static_cast<int>(blocks);
     if (nchunks <= 64) launch_gemv_vec<ODT, MR, RPW, 1>(q, w, xs, ws, ws_size, bias, res, out, N, K, gelu, b, stream);
