@@ -131,6 +131,94 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
     }
 }
 
+// Grid-stride form of quant_rows_vec (RPW = 1) for rows of several waves:
+// wave group g of the grid quantizes rows g, g + G, g + 2 G, ... (G = wave
+// groups in the grid) and loads its next row while reducing and storing the
+// current one, so each wave keeps two rows' loads in flight.  The iteration
+// count is the same for every wave of the grid (rows past M are masked), as
+// the cross-wave absmax exchange is a block barrier.
+template <int DT, int W, int CPL, bool GELU, bool SCALES_ONLY>
+__global__ __launch_bounds__(256) void quant_rows_stream(const void* __restrict__ xv, int8_t* __restrict__ q,
+                                                         float* __restrict__ xs, int64_t M, int64_t K, int recip) {
+    using D = DType<DT>;
+    constexpr int E = 16 / D::bytes;
+    constexpr int GROUPS = 4 / W;
+    const int tid = threadIdx.x % (kWave * W);
+    const int grp = threadIdx.x / (kWave * W);
+    const int wave = threadIdx.x / kWave;
+    const int64_t G = static_cast<int64_t>(gridDim.x) * GROUPS;
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * GROUPS + grp;
+    const int64_t iters = (M + G - 1) / G;
+    const int64_t nchunks = K / E;
+    __shared__ float wave_amax[2][4];   // by iteration parity: no barrier between write rounds
+
+    auto load_row = [&](uint4 (&raw)[CPL], int64_t row) {
+        const bool ok = row < M;
+        const uint4* src = reinterpret_cast<const uint4*>(static_cast<const char*>(xv) + (ok ? row : 0) * K * D::bytes);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int64_t c = tid + static_cast<int64_t>(j) * kWave * W;
+            raw[j] = (ok && c < nchunks) ? src[c] : make_uint4(0, 0, 0, 0);
+        }
+    };
+    uint4 cur[CPL], nxt[CPL];
+    load_row(cur, g);
+    for (int64_t it = 0; it < iters; ++it) {
+        const int64_t row = g + it * G;
+        if (it + 1 < iters) load_row(nxt, row + G);
+        if constexpr (GELU) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                uint32_t* wv = reinterpret_cast<uint32_t*>(&cur[j]);
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    if constexpr (D::bytes == 4) wv[h] = __float_as_uint(gelu_f32(__uint_as_float(wv[h])));
+                    else wv[h] = gelu_x2<DT>(wv[h]);
+                }
+            }
+        }
+        auto elem = [&](int j, int i) {
+            const typename D::storage* e = reinterpret_cast<const typename D::storage*>(&cur[j]);
+            return D::load(e[i]);
+        };
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+            for (int i = 0; i < E; ++i) m = fmaxf(m, fabsf(elem(j, i)));
+        float amax = wave_max(m);
+        const int par = static_cast<int>(it & 1);
+        if ((threadIdx.x % kWave) == 0) wave_amax[par][wave] = amax;
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < W; ++w) amax = fmaxf(amax, wave_amax[par][grp * W + w]);
+        if (row < M) {
+            const float s = row_scale<DT>(amax, recip != 0);
+            if (tid == 0) xs[row] = s;
+            if constexpr (!SCALES_ONLY) {
+                const RowQuant rq = row_quant<DT>(s);
+                int8_t* dst = q + row * K;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const int64_t c = tid + static_cast<int64_t>(j) * kWave * W;
+                    if (c >= nchunks) break;
+                    if constexpr (E == 8) {
+                        uint2 packed;
+                        packed.x = quant4_packed<DT>(elem(j, 0), elem(j, 1), elem(j, 2), elem(j, 3), rq);
+                        packed.y = quant4_packed<DT>(elem(j, 4), elem(j, 5), elem(j, 6), elem(j, 7), rq);
+                        *reinterpret_cast<uint2*>(dst + c * E) = packed;
+                    } else {
+                        *reinterpret_cast<uint32_t*>(dst + c * E) =
+                            quant4_packed<DT>(elem(j, 0), elem(j, 1), elem(j, 2), elem(j, 3), rq);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) cur[j] = nxt[j];
+    }
+}
+
 // Any K, any alignment: one block per row, element loads, two passes.
 template <int DT, bool GELU, bool SCALES_ONLY>
 __global__ __launch_bounds__(256) void quant_rows_generic(const void* __restrict__ xv,
@@ -166,15 +254,26 @@ template <int DT, int W, int CPL, int RPW, bool GELU, bool SO>
 static void launch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, int recip,
                        hipStream_t stream) {
     const int64_t rows = (4 / W) * RPW;
+    // Rows of several waves stream: two rows per wave group (M = 11712 bf16:
+    // K = 3072 24.3 -> 23.5 us, K = 12288 83.7 -> 81.0 us; three or six rows
+    // per group measured no better).
+    constexpr int kStreamRows = 2;
+    if constexpr (W > 1) {
+        const int64_t per_block = (4 / W) * kStreamRows;
+        const dim3 grid(static_cast<unsigned>((M + per_block - 1) / per_block));
+        hipLaunchKernelGGL((quant_rows_stream<DT, W, CPL, GELU, SO>), grid, dim3(256), 0, stream, x, q, xs, M, K,
+                           recip);
+        return;
+    }
     const dim3 grid(static_cast<unsigned>((M + rows - 1) / rows));
     hipLaunchKernelGGL((quant_rows_vec<DT, W, CPL, RPW, GELU, SO>), grid, dim3(256), 0, stream, x, q,
                        xs, M, K, recip);
 }
 
-// Rows of up to 128 chunks take one wave each; longer rows two or four waves,
-// which keeps more waves streaming per row (K = 3072 bf16, 384 chunks: two
-// waves of 3 chunks per lane, every lane busy, ~23.3 us; four waves of 2,
-// ~24.6 us; one wave of 6, 26.1 us; a plain copy of the same bytes 21.8 us).
+// Rows of up to 128 chunks take one wave each; longer rows two or four waves
+// in the streaming kernel (K = 3072 bf16, 384 chunks: two waves of 3 chunks
+// per lane, every lane busy; four waves of 2 and one wave of 6 measured
+// slower; a plain copy of the same bytes 21.8 us).
 template <int DT, bool GELU, bool SO>
 static bool dispatch_vec(const void* x, int8_t* q, float* xs, int64_t M, int64_t K, int recip,
                          hipStream_t stream) {
