@@ -18,6 +18,8 @@ ROUTE_GEMM = 1 << 4
 GIVEN_SCALE = 1 << 5
 # input activation codes
 ACT_CODES = {None: 0, "gelu_tanh": 1, "swiglu": 2, "rms_norm": 3, "situ": 4}
+# w8a8_adaln mode bits
+ADALN_RMS, ADALN_SINGLE_ROUNDING = 1, 2
 # GEMM main loops (flag bits 8..11: GEMM_TILE(code))
 TILE_AUTO, TILE_256x192, TILE_256x256, TILE_384x192, TILE_256x128, TILE_REGS, TILE_GENERIC = range(7)
 TILE_NAMES = {TILE_AUTO: "auto", TILE_256x192: "256x192", TILE_256x256: "256x256", TILE_384x192: "384x192",

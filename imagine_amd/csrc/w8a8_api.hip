@@ -41,7 +41,7 @@ bool convrot_weight_fused(const void* w, const void* q, int64_t K, int64_t group
 void launch_quantize_tensorwise(const void* x, int x_dtype, int8_t* q, float* scale, int64_t n, bool given,
                                 bool recip, hipStream_t stream);
 void launch_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
-                  int64_t sg, int64_t tg, float eps, int dtype, bool rms, hipStream_t stream);
+                  int64_t sg, int64_t tg, float eps, int dtype, bool rms, bool single, hipStream_t stream);
 void launch_gated_residual(const void* x, const void* y, const void* gate0, const void* gate1, void* out,
                            int64_t batch, int64_t tokens, int64_t d, int64_t prefix, int dtype,
                            hipStream_t stream);
@@ -209,9 +209,10 @@ int w8a8_adaln(const void* x, const void* scale, const void* shift, void* out, i
     if (n == 0) return W8A8_OK;
     if (!x || !scale || !shift || !out) return fail(W8A8_ERR_VALUE, "null tensor pointer");
     if (n > 0x7fffffff) return fail(W8A8_ERR_VALUE, "adaln supports at most 2^31 - 1 rows");
+    if (rms & ~(W8A8_ADALN_RMS | W8A8_ADALN_SINGLE_ROUNDING)) return fail(W8A8_ERR_VALUE, "unknown adaln mode bits");
     w8a8::launch_adaln(x, scale, shift, out, n, d, scale_group, shift_group, static_cast<float>(eps), dtype,
-                       rms != 0, stream);
-    return check_launch(rms ? "rms_adaln" : "adaln");
+                       (rms & W8A8_ADALN_RMS) != 0, (rms & W8A8_ADALN_SINGLE_ROUNDING) != 0, stream);
+    return check_launch((rms & W8A8_ADALN_RMS) ? "rms_adaln" : "adaln");
 }
 
 int w8a8_modulated_norm_quant(const void* x, const void* scale0, const void* scale1, const void* shift0,

@@ -54,7 +54,10 @@ __device__ __forceinline__ float block_sum(float v, float* part) {
     return (part[0] + part[1]) + (part[2] + part[3]);
 }
 
-template <int DT, bool RMS>
+// SINGLE: the single-rounding form T(fma(norm, 1 + scale, shift)) in fp32
+// (the structure of Kitchen's CUDA adaln kernel, adaln.cu in the reference's
+// native-source archive), instead of the eager route's three roundings.
+template <int DT, bool RMS, bool SINGLE>
 __global__ __launch_bounds__(kGlueThreads) void adaln_rows(const void* __restrict__ x,
                                                            const void* __restrict__ scale,
                                                            const void* __restrict__ shift,
@@ -95,17 +98,22 @@ __global__ __launch_bounds__(kGlueThreads) void adaln_rows(const void* __restric
     const float bias = -rstd * mean;   // aten's y = x * rstd + (-rstd * mean)
     for (int64_t k = threadIdx.x; k < d; k += kGlueThreads) {
         const float v = D::load(xr[k]);
-        const float y = D::round(RMS ? v * rstd : fmaf(v, rstd, bias));
-        const float m = D::round(1.0f + D::load(sr[k]));
-        const float z = D::round(y * m);
-        o[k] = D::store(z + D::load(hr[k]));
+        if constexpr (SINGLE) {
+            const float y = RMS ? v * rstd : fmaf(v, rstd, bias);
+            o[k] = D::store(fmaf(y, 1.0f + D::load(sr[k]), D::load(hr[k])));
+        } else {
+            const float y = D::round(RMS ? v * rstd : fmaf(v, rstd, bias));
+            const float m = D::round(1.0f + D::load(sr[k]));
+            const float z = D::round(y * m);
+            o[k] = D::store(z + D::load(hr[k]));
+        }
     }
 }
 
 // Register-resident adaln: lane chunk c = tid + j * 256 of the row (E values
 // per 16-byte chunk); same operations per element as adaln_rows, so the same
 // results up to the order of the fp32 row sums.
-template <int DT, bool RMS, int CPL, int NT>
+template <int DT, bool RMS, bool SINGLE, int CPL, int NT>
 __global__ __launch_bounds__(NT) void adaln_rows_vec(const void* __restrict__ x,
                                                                const void* __restrict__ scale,
                                                                const void* __restrict__ shift,
@@ -176,10 +184,15 @@ __global__ __launch_bounds__(NT) void adaln_rows_vec(const void* __restrict__ x,
 #pragma unroll
         for (int i = 0; i < E; ++i) {
             const float v = elem(raw[j], i);
-            const float y = D::round(RMS ? v * rstd : fmaf(v, rstd, bias));
-            const float m = D::round(1.0f + elem(sv, i));
-            const float z = D::round(y * m);
-            rp[i] = D::store(z + elem(hv, i));
+            if constexpr (SINGLE) {
+                const float y = RMS ? v * rstd : fmaf(v, rstd, bias);
+                rp[i] = D::store(fmaf(y, 1.0f + elem(sv, i), elem(hv, i)));
+            } else {
+                const float y = D::round(RMS ? v * rstd : fmaf(v, rstd, bias));
+                const float m = D::round(1.0f + elem(sv, i));
+                const float z = D::round(y * m);
+                rp[i] = D::store(z + elem(hv, i));
+            }
         }
         o[c] = res;
     }
@@ -353,11 +366,11 @@ __device__ __forceinline__ void store_pair(typename DType<DT>::storage* o, int64
 }
 
 template <int DT, int PPL, bool PAIR, bool NORM>
-__global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ q, const void* __restrict__ k,
+__global__ __launch_bounds__(256) void rms_rope_tokens(const void* q, const void* k,
                                                        const float* __restrict__ freqs,
                                                        const void* __restrict__ q_scale,
-                                                       const void* __restrict__ k_scale, void* __restrict__ q_out,
-                                                       void* __restrict__ k_out, int64_t tokens, int64_t seq,
+                                                       const void* __restrict__ k_scale, void* q_out,
+                                                       void* k_out, int64_t tokens, int64_t seq,
                                                        int64_t heads, int64_t d, int64_t x_stride,
                                                        int64_t o_stride, int ntensors, int freq_per_batch,
                                                        float eps) {
@@ -388,7 +401,6 @@ __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ 
             }
         }
     }
-    const float inv_d = 1.0f / static_cast<float>(d);
     for (int64_t h0 = 0; h0 < heads; h0 += kHeadGroup) {
         float a[kHeadGroup][PPL], c[kHeadGroup][PPL], sum[kHeadGroup];
 #pragma unroll
@@ -413,7 +425,7 @@ __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ 
 #pragma unroll
         for (int g = 0; g < kHeadGroup; ++g) {
             if (h0 + g >= heads) break;
-            const float r = NORM ? 1.0f / sqrtf(sum[g] * inv_d + eps) : 1.0f;
+            const float r = NORM ? 1.0f / sqrtf(sum[g] / static_cast<float>(d) + eps) : 1.0f;
 #pragma unroll
             for (int j = 0; j < PPL; ++j) {
                 const int64_t p = lane + j * kWave;
@@ -435,11 +447,11 @@ __global__ __launch_bounds__(256) void rms_rope_tokens(const void* __restrict__ 
 // registers for the whole token.  Same numerics per element as
 // rms_rope_tokens (the fp32 row sum adds in another order).
 template <int DT, int LPR, bool NORM>
-__global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restrict__ q, const void* __restrict__ k,
+__global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* q, const void* k,
                                                            const float* __restrict__ freqs,
                                                            const void* __restrict__ q_scale,
                                                            const void* __restrict__ k_scale,
-                                                           void* __restrict__ q_out, void* __restrict__ k_out,
+                                                           void* q_out, void* k_out,
                                                            int64_t tokens, int64_t seq, int64_t heads,
                                                            int64_t x_stride, int64_t o_stride, int ntensors,
                                                            int freq_per_batch, float eps) {
@@ -471,7 +483,6 @@ __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restric
             w[2 * i + 1] = D::load(static_cast<uint16_t>(ww[i] >> 16));
         }
     }
-    const float inv_d = 1.0f / static_cast<float>(d);
     for (int64_t h0 = 0; h0 < heads; h0 += kRows * kGroup) {
         float v[kGroup][8], sum[kGroup];
 #pragma unroll
@@ -500,7 +511,7 @@ __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restric
         for (int g = 0; g < kGroup; ++g) {
             const int64_t h = h0 + g * kRows + sub;
             if (h >= heads) continue;
-            const float r = NORM ? 1.0f / sqrtf(sum[g] * inv_d + eps) : 1.0f;
+            const float r = NORM ? 1.0f / sqrtf(sum[g] / static_cast<float>(d) + eps) : 1.0f;
             uint32_t out[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -516,7 +527,7 @@ __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* __restric
 // x[b, t, :] += y[b, t, :] * gate[b, :], gate = gate0 for t < prefix else gate1;
 // gates are [batch, d].  out may alias x (the reference updates x in place).
 template <int DT>
-__global__ __launch_bounds__(kGlueThreads) void gated_residual_rows(const void* __restrict__ x,
+__global__ __launch_bounds__(kGlueThreads) void gated_residual_rows(const void* x,
                                                                     const void* __restrict__ y,
                                                                     const void* __restrict__ gate0,
                                                                     const void* __restrict__ gate1,
@@ -541,7 +552,7 @@ __global__ __launch_bounds__(kGlueThreads) void gated_residual_rows(const void* 
 // The same over 16-byte chunks (d % E == 0, 16-byte aligned operands): chunk
 // c of the [rows, d] tensor lies in row c / (d / E).
 template <int DT>
-__global__ __launch_bounds__(kGlueThreads) void gated_residual_vec(const uint4* __restrict__ x,
+__global__ __launch_bounds__(kGlueThreads) void gated_residual_vec(const uint4* x,
                                                                    const uint4* __restrict__ y,
                                                                    const uint4* __restrict__ gate0,
                                                                    const uint4* __restrict__ gate1,
@@ -601,18 +612,18 @@ namespace {
 // Rows of up to 1024 16-byte chunks take 128 threads (2 waves), longer rows
 // 256: at the DiT width (3072 bf16 = 384 chunks) every lane then holds 3
 // chunks, where 256 threads would leave a quarter of them idle.
-template <int DT, bool RMS, int CPL>
+template <int DT, bool RMS, bool SINGLE, int CPL>
 void launch_adaln_vec(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
                       int64_t sg, int64_t tg, float eps, bool narrow, hipStream_t stream) {
     if (narrow)
-        hipLaunchKernelGGL((adaln_rows_vec<DT, RMS, CPL, 128>), dim3(static_cast<unsigned>(n)), dim3(128), 0,
+        hipLaunchKernelGGL((adaln_rows_vec<DT, RMS, SINGLE, CPL, 128>), dim3(static_cast<unsigned>(n)), dim3(128), 0,
                            stream, x, scale, shift, out, d, sg, tg, eps);
     else
-        hipLaunchKernelGGL((adaln_rows_vec<DT, RMS, CPL, 256>), dim3(static_cast<unsigned>(n)), dim3(256), 0,
+        hipLaunchKernelGGL((adaln_rows_vec<DT, RMS, SINGLE, CPL, 256>), dim3(static_cast<unsigned>(n)), dim3(256), 0,
                            stream, x, scale, shift, out, d, sg, tg, eps);
 }
 
-template <int DT, bool RMS>
+template <int DT, bool RMS, bool SINGLE>
 bool adaln_vec_dispatch(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
                         int64_t sg, int64_t tg, float eps, hipStream_t stream) {
     constexpr int E = 16 / DType<DT>::bytes;
@@ -622,14 +633,14 @@ bool adaln_vec_dispatch(const void* x, const void* scale, const void* shift, voi
     const int nt = narrow ? 128 : 256;
     const int64_t per_lane = (d / E + nt - 1) / nt;
     switch (per_lane) {
-        case 1: launch_adaln_vec<DT, RMS, 1>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
-        case 2: launch_adaln_vec<DT, RMS, 2>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
-        case 3: launch_adaln_vec<DT, RMS, 3>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
-        case 4: launch_adaln_vec<DT, RMS, 4>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 1: launch_adaln_vec<DT, RMS, SINGLE, 1>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 2: launch_adaln_vec<DT, RMS, SINGLE, 2>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 3: launch_adaln_vec<DT, RMS, SINGLE, 3>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 4: launch_adaln_vec<DT, RMS, SINGLE, 4>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
         case 5:
-        case 6: launch_adaln_vec<DT, RMS, 6>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 6: launch_adaln_vec<DT, RMS, SINGLE, 6>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
         case 7:
-        case 8: launch_adaln_vec<DT, RMS, 8>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
+        case 8: launch_adaln_vec<DT, RMS, SINGLE, 8>(x, scale, shift, out, n, d, sg, tg, eps, narrow, stream); return true;
         default: return false;
     }
 }
@@ -687,22 +698,34 @@ bool launch_modnorm_quant(const void* x, const void* s0, const void* s1, const v
     return false;
 }
 
+namespace {
+
+template <int DT, bool RMS, bool SINGLE>
+void adaln_dispatch(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
+                    int64_t sg, int64_t tg, float eps, hipStream_t stream) {
+    if (adaln_vec_dispatch<DT, RMS, SINGLE>(x, scale, shift, out, n, d, sg, tg, eps, stream)) return;
+    hipLaunchKernelGGL((adaln_rows<DT, RMS, SINGLE>), dim3(static_cast<unsigned>(n)), dim3(kGlueThreads), 0, stream,
+                       x, scale, shift, out, d, sg, tg, eps);
+}
+
+template <int DT>
+void adaln_dispatch_dt(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
+                       int64_t sg, int64_t tg, float eps, bool rms, bool single, hipStream_t stream) {
+    if (rms && single) adaln_dispatch<DT, true, true>(x, scale, shift, out, n, d, sg, tg, eps, stream);
+    else if (rms) adaln_dispatch<DT, true, false>(x, scale, shift, out, n, d, sg, tg, eps, stream);
+    else if (single) adaln_dispatch<DT, false, true>(x, scale, shift, out, n, d, sg, tg, eps, stream);
+    else adaln_dispatch<DT, false, false>(x, scale, shift, out, n, d, sg, tg, eps, stream);
+}
+
+}  // namespace
+
 void launch_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
-                  int64_t sg, int64_t tg, float eps, int dtype, bool rms, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(n)), block(kGlueThreads);
-#define W8A8_ADALN_CASE(DT)                                                                            \
-    if (dtype == DT) {                                                                                 \
-        if (rms ? adaln_vec_dispatch<DT, true>(x, scale, shift, out, n, d, sg, tg, eps, stream)        \
-                : adaln_vec_dispatch<DT, false>(x, scale, shift, out, n, d, sg, tg, eps, stream))      \
-            return;                                                                                    \
-        if (rms) hipLaunchKernelGGL((adaln_rows<DT, true>), grid, block, 0, stream, x, scale, shift, out, d, sg, tg, eps); \
-        else hipLaunchKernelGGL((adaln_rows<DT, false>), grid, block, 0, stream, x, scale, shift, out, d, sg, tg, eps);    \
-        return;                                                                                        \
+                  int64_t sg, int64_t tg, float eps, int dtype, bool rms, bool single, hipStream_t stream) {
+    switch (dtype) {
+        case W8A8_BF16: adaln_dispatch_dt<W8A8_BF16>(x, scale, shift, out, n, d, sg, tg, eps, rms, single, stream); return;
+        case W8A8_F16: adaln_dispatch_dt<W8A8_F16>(x, scale, shift, out, n, d, sg, tg, eps, rms, single, stream); return;
+        default: adaln_dispatch_dt<W8A8_F32>(x, scale, shift, out, n, d, sg, tg, eps, rms, single, stream); return;
     }
-    W8A8_ADALN_CASE(W8A8_BF16)
-    W8A8_ADALN_CASE(W8A8_F16)
-    W8A8_ADALN_CASE(W8A8_F32)
-#undef W8A8_ADALN_CASE
 }
 
 void launch_gated_residual(const void* x, const void* y, const void* gate0, const void* gate1, void* out,

@@ -46,10 +46,12 @@ def _modulation(t, x, n, d):
     return t.expand_as(x).reshape(n, d).contiguous(), 1
 
 
-def adaln(x, scale, shift, eps, rms=False):
+def adaln(x, scale, shift, eps, rms=False, single_rounding=False):
     """Kitchen's ``adaln`` / ``rms_adaln`` as the crate calls them on the GPU:
-    ``T(T(T(norm(x)) * T(1 + scale)) + shift)`` over the last dimension, scale
-    and shift broadcast by ``_modulation``, in x's dtype."""
+    ``T(T(T(norm(x)) * T(1 + scale)) + shift)`` over the last dimension (the
+    crate's eager op order), scale and shift broadcast by ``_modulation``, in
+    x's dtype.  ``single_rounding``: ``T(fma(norm, 1 + scale, shift))`` in fp32
+    instead, the rounding structure of Kitchen's CUDA kernel."""
     shape = x.shape
     if len(shape) == 0:
         raise IndexError("tuple index out of range")
@@ -67,17 +69,17 @@ def adaln(x, scale, shift, eps, rms=False):
     out = torch.empty_like(inp)
     _lib.check(_lib.load().w8a8_adaln(
         _ptr(inp), _ptr(sc), _ptr(sh), _ptr(out), n, d, sg, tg, float(eps), _dtype_code(x.dtype, "adaln"),
-        1 if rms else 0, _stream(x.device)))
+        (_lib.ADALN_RMS if rms else 0) | (_lib.ADALN_SINGLE_ROUNDING if single_rounding else 0), _stream(x.device)))
     return out.reshape(shape)
 
 
-def modulated_norm(x, scale, prefix, zero, eps, rms=False):
+def modulated_norm(x, scale, prefix, zero, eps, rms=False, single_rounding=False):
     """numeric.rs:63-107 (inference branch): adaln of every token with
     ``scale[1]``, then the first ``prefix`` tokens (dimension 1) again with
     ``scale[0]``; shift ``zero``.  ``rms`` selects rms_adaln."""
-    out = adaln(x, scale[1], zero, eps, rms=rms)
+    out = adaln(x, scale[1], zero, eps, rms=rms, single_rounding=single_rounding)
     if prefix != 0:
-        out[:, :prefix].copy_(adaln(x[:, :prefix], scale[0], zero, eps, rms=rms))
+        out[:, :prefix].copy_(adaln(x[:, :prefix], scale[0], zero, eps, rms=rms, single_rounding=single_rounding))
     return out
 
 

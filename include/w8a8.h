@@ -328,16 +328,25 @@ int w8a8_quantize_convrot_weight(const void* w, int w_dtype, int8_t* q, float* s
 
 /* ---- DiT block glue around the linears ------------------------------------ */
 
+/* Mode bits of w8a8_adaln's `rms` argument (0 / 1 keep their meaning). */
+#define W8A8_ADALN_RMS 1             /* RMSNorm instead of LayerNorm */
+#define W8A8_ADALN_SINGLE_ROUNDING 2 /* out = T(fma(norm, 1 + scale, shift)) in fp32 */
+
 /* Adaptive LayerNorm / RMSNorm with modulation, Kitchen's native "adaln" and
  * "rms_adaln" calls as the crate issues them (inference/src/backend_eager.rs:
  * 176-229: input [n, d], scale [n / scale_group, d], shift [n / shift_group, d],
  * out, n, d, sg, tg, eps, dtype): row i gets scale row i / scale_group and
  * shift row i / shift_group, and
  *   out = T( T( T(norm(x)) * T(1 + scale) ) + shift ),
- * norm = layer_norm without affine (biased variance) or, with rms != 0,
- * x * rsqrt(mean(x^2) + eps), in fp32: the op order of the crate's eager
- * route (:186-199).  d == 0 fails with the reference's ZeroDivisionError
- * text as W8A8_ERR_VALUE. */
+ * norm = layer_norm without affine (biased variance) or, with
+ * W8A8_ADALN_RMS, x * rsqrt(mean(x^2) + eps), in fp32: the op order of the
+ * crate's eager route (:186-199).  W8A8_ADALN_SINGLE_ROUNDING gives instead
+ * the single rounding of Kitchen's CUDA kernel (adaln.cu in the reference's
+ * design/reference-local/native-source-candidates.tar.gz: fp32 statistics,
+ * (x - mean) * rstd * (1 + scale) + shift rounded once); that kernel's row
+ * sums and its approximate rsqrt are not restated, so outputs agree with it
+ * to an ulp, not bit for bit.  d == 0 fails with the reference's
+ * ZeroDivisionError text as W8A8_ERR_VALUE. */
 int w8a8_adaln(const void* x, const void* scale, const void* shift, void* out, int64_t n, int64_t d,
                int64_t scale_group, int64_t shift_group, double eps, int dtype, int rms,
                hipStream_t stream);

@@ -295,6 +295,25 @@ def gated_residual(x, y, g, dtype):
     return to_dtype(v, dtype)
 
 
+def adaln_single(x, scale, shift, eps, dtype, rms=False):
+    """The single-rounding adaLN (the rounding structure of Kitchen's CUDA
+    kernel, adaln.cu in the reference's native-source archive):
+    T(fp32(y * fp32(1 + scale) + shift)) with y the fp32 normalised value and
+    the multiply-add fused; the norm in float64 here, so this matches a fp32
+    implementation to within one ulp of T."""
+    xf = to_f32(x, dtype).astype(np.float64)
+    if rms:
+        y = xf / np.sqrt((xf * xf).mean(axis=-1, keepdims=True) + eps)
+    else:
+        mu = xf.mean(axis=-1, keepdims=True)
+        var = ((xf - mu) ** 2).mean(axis=-1, keepdims=True)
+        y = (xf - mu) / np.sqrt(var + eps)
+    y = y.astype(np.float32).astype(np.float64)
+    m = (np.float32(1.0) + to_f32(scale, dtype)).astype(np.float32).astype(np.float64)
+    z = (y * m + to_f32(shift, dtype).astype(np.float64)).astype(np.float32)   # one rounding: fma
+    return to_dtype(z, dtype)
+
+
 def adaln(x, scale, shift, eps, dtype, rms=False):
     """backend_eager.rs:186-199 in float64 up to the roundings of the op order:
     y = T(norm(x)), T(y * T(1 + scale)), T(. + shift); x [n, d], scale and shift

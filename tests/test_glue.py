@@ -89,6 +89,34 @@ def test_adaln_oracle_is_a_normalisation():
     assert np.allclose((rms * rms).mean(-1), 1, atol=1e-4)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("rms", [False, True])
+def test_adaln_single_rounding_oracle_against_fp32_torch(dtype, rms):
+    """oracle.adaln_single against an independent fp32 evaluation of the same
+    formula with ATen (layer_norm / rms_norm in fp32, then y * (1 + scale) +
+    shift in fp32, rounded to T once): within one ulp of T, almost all
+    bit-equal (the fp32 norm and the unfused multiply-add round differently in
+    rare cases); and, with zero modulation, the same as rounding the norm."""
+    g = torch.Generator().manual_seed(35)
+    x = (torch.randn(48, 3072, generator=g) * 2 + 0.3).to(TD[dtype])
+    scale = (torch.randn(1, 3072, generator=g) * 0.5).to(TD[dtype])
+    shift = (torch.randn(1, 3072, generator=g) * 0.1).to(TD[dtype])
+    xf = x.float()
+    y = torch.nn.functional.rms_norm(xf, (3072,), eps=1e-6) if rms else torch.nn.functional.layer_norm(xf, (3072,), eps=1e-6)
+    want = storage((y * (1 + scale.float()) + shift.float()).to(TD[dtype]), dtype)
+    got = O.adaln_single(storage(x, dtype), storage(scale, dtype), storage(shift, dtype), 1e-6, dtype, rms)
+    a, b = O.to_f32(got, dtype).astype(np.float64), O.to_f32(want, dtype).astype(np.float64)
+    z = (y * (1 + scale.float())).numpy().astype(np.float64)   # before the shift, which may cancel it
+    rel = {"bf16": 2.0**-7, "f16": 2.0**-10}[dtype]
+    assert np.all(np.abs(a - b) <= np.maximum(np.abs(b), np.abs(z)) * rel + 1e-6)
+    assert (got == want).mean() > 0.99
+    zero = np.zeros((1, 3072), np.uint16)
+    got0 = O.adaln_single(storage(x, dtype), zero, zero, 1e-6, dtype, rms)
+    assert (got0 == storage(y.to(TD[dtype]), dtype)).mean() > 0.99
+    # a dropped "1 +" or a sign slip would be far off
+    assert not np.array_equal(got, O.adaln_single(storage(x, dtype), storage(scale, dtype), zero, 1e-6, dtype, rms))
+
+
 def test_modulation_grouping_follows_the_reference_rule():
     x = torch.zeros(2, 5, 8)
     t, grp = _modulation(torch.ones(2, 1, 8), x, 10, 8)
