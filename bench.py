@@ -25,6 +25,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -116,10 +117,43 @@ def median_of_batches(fn, warmup=20, batches=7, calls=30):
     return statistics.median(means)
 
 
+def host_cpu():
+    """nproc and the lscpu model / core / thread counts of the host."""
+    info = {"nproc": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        keys = {"Model name": "model", "CPU(s)": "cpus", "Thread(s) per core": "threads_per_core",
+                "Core(s) per socket": "cores_per_socket", "Socket(s)": "sockets"}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in keys:
+                info[keys[k.strip()]] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
+def cpu_time_per_call(fn, warmup=20, batches=7, calls=30):
+    """The reference's method on the host: 20 warmups, 7 batches x 30 calls,
+    median of batch means (experiments/.../INT8-KITCHEN.md:35-39); seconds."""
+    for _ in range(warmup):
+        fn()
+    means = []
+    for _ in range(batches):
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        means.append((time.perf_counter() - t0) / calls)
+    return statistics.median(means)
+
+
 def cpu_baseline(seconds):
     """The reference's LibTorch-CPU route (oracle/torch_eager.py, same ATen op
-    sequence as inference/src/int8_linear.rs:198-277) on a bounded sample of the
-    same workload: the 4 block linears at M=256 rows, repeated for ~`seconds`."""
+    sequence as inference/src/int8_linear.rs:198-277), timed on the host's
+    cores: the headline value on a bounded sample of the bench's workload (the
+    4 block linears at M=256 rows, repeated for ~`seconds`), and the two
+    CPU-sized configurations with the reference's timing method: the single
+    linear M=256 K=3072 N=3072 and the adaLN GEMV M=2 K=3072 N=18432."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import torch_eager as TE
     torch.set_num_threads(os.cpu_count() or 1)
@@ -144,18 +178,29 @@ def cpu_baseline(seconds):
         if el >= seconds:
             break
     tops = ops_per_pass * passes / el / 1e12
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    host = host_cpu()
+
+    # the two CPU configurations, 20 warmups + 7 x 30 calls each
+    k, n = 3072, 3072
+    w, ws, b = make_linear(k, n, 300, "cpu")
+    x = torch.randn(256, k, generator=gen(301)).to(torch.bfloat16)
+    t_c1 = cpu_time_per_call(lambda: TE.int8_linear(x, w, ws, b, torch.bfloat16))
+    k, n = 3072, 18432
+    w2, ws2, b2 = make_linear(k, n, 302, "cpu")
+    x2 = torch.randn(2, k, generator=gen(303)).to(torch.bfloat16)
+    t_c2 = cpu_time_per_call(lambda: TE.int8_linear(x2, w2, ws2, b2, torch.bfloat16))
+    gemv_bytes = n * k + 2 * k * 2 + 2 * n * 2 + n * 4   # weights, x, out, scales
     return {"value": round(tops, 4), "unit": "TOPS", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"block linear set (QKV, out, up, down) at M=256 tokens, {passes} passes "
-                      f"in {el:.1f} s, LibTorch CPU int8_linear op sequence; host {model}"}
+                      f"in {el:.1f} s, LibTorch CPU int8_linear op sequence; host {host.get('model', '')}",
+            "host": host,
+            "single_linear_M256_K3072_N3072": {"ms": round(t_c1 * 1e3, 3),
+                                               "TOPS": round(2 * 256 * 3072 * 3072 / t_c1 / 1e12, 4),
+                                               "method": "20 warmups, median of 7 x 30 calls"},
+            "adaln_gemv_M2_K3072_N18432": {"ms": round(t_c2 * 1e3, 3),
+                                           "GB/s": round(gemv_bytes / t_c2 / 1e9, 2),
+                                           "method": "20 warmups, median of 7 x 30 calls"}}
 
 
 def main():
