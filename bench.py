@@ -46,7 +46,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--only", default=None,
                    help="run only one kernel in a loop (for rocprofv3 counters): "
-                        "up_gemm | quant | convrot_quant | rms_rope | step | copy | dit_step")
+                        "up_gemm | quant | quant12288 | gemv | convrot_quant | rms_rope | step | copy | dit_step")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-dit-step", action="store_true", help="skip the 60-block DiT step extra")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -558,6 +558,24 @@ def run_only(args, W, lib, dev, layers, step, quant, gemm, qbuf, x_ffn, outs):
     elif args.only == "quant":
         for _ in range(n_iter):
             quant(x_ffn, qbuf[HID])
+    elif args.only == "quant12288":
+        x12 = torch.randn(M_TOK, FFN, device=dev).to(torch.bfloat16)
+        q12 = torch.empty(M_TOK, FFN, dtype=torch.int8, device=dev)
+        s12 = torch.empty(M_TOK, dtype=torch.float32, device=dev)
+        for _ in range(n_iter):
+            W._lib.check(lib.w8a8_quantize_rowwise(x12.data_ptr(), W._lib.BF16, q12.data_ptr(), s12.data_ptr(),
+                                                   M_TOK, FFN, 0, torch.cuda.current_stream().cuda_stream))
+    elif args.only == "gemv":
+        # adaLN GEMV M=2 K=3072 N=18432 (one weight; the timed extra rotates 8)
+        m, k, n = 2, HID, 6 * HID
+        w, ws, b = make_linear(k, n, 40, dev)
+        qg = torch.randint(-127, 128, (m, k), device=dev, dtype=torch.int8)
+        xsg = torch.rand(m, device=dev) * 1e-2
+        og = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        for _ in range(n_iter):
+            W._lib.check(lib.w8a8_gemv_dequant(qg.data_ptr(), w.data_ptr(), xsg.data_ptr(), ws.data_ptr(), n,
+                                               b.data_ptr(), og.data_ptr(), W._lib.BF16, m, n, k, 0,
+                                               torch.cuda.current_stream().cuda_stream))
     elif args.only == "convrot_quant":
         s = torch.empty(M_TOK, dtype=torch.float32, device=dev)
         for _ in range(n_iter):
