@@ -117,12 +117,15 @@ template <> struct DType<W8A8_BF16> {
 //                                            subtraction rounds like an fp32
 //                                            tanh, so 1 + tanh u cancels as it
 //                                            does: exactly 0 once |u| > 9)
-//   gelu = (x/2) (1 + copysign(r, x))       (the reference's two roundings:
-//                                            a single fma would turn the -0 of
-//                                            the saturated negative tail into +0)
+//   gelu = x (1/2 + copysign(1/2, x) r)     (= (x/2) RN(1 + copysign(r, x)),
+//                                            the reference's two roundings, for
+//                                            every x: halving commutes with
+//                                            rounding here, and x/2 is exact;
+//                                            the saturated negative tail gives
+//                                            x * +0 = -0 as the reference does)
 // exp2 and the reciprocal are the hardware approximations (about 1 ulp); the
 // fp32 result carries a few ulps of error, which bf16 rounding never shows.
-// About 14 VALU slots; it runs in the FFN-up epilogue while the matrix cores
+// About 13 VALU slots; it runs in the FFN-up epilogue while the matrix cores
 // idle, where a table lookup measured 12-18% slower on the whole GEMM.
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
     const float kA = 2.302208198144325f;      // sqrt(2/pi) * 2 / ln 2
@@ -131,7 +134,7 @@ __device__ __forceinline__ float gelu_tanh_fast(float x) {
     const float t = __builtin_amdgcn_exp2f(-fabsf(e));   // (0, 1]
     const float q = t * __builtin_amdgcn_rcpf(1.0f + t);
     const float r = fmaf(-2.0f, q, 1.0f);
-    return (0.5f * x) * (1.0f + __builtin_copysignf(r, x));
+    return x * fmaf(__builtin_copysignf(0.5f, x), r, 0.5f);
 }
 
 // Two bf16 values packed in one word (low half first) -> their GELU, rounded

@@ -29,8 +29,10 @@ int device_cus() {
 // Default tile choice among the three one-block-per-CU configurations: the
 // estimated time of a shape is (rounds of tiles over the CUs) x (tile area),
 // divided by the configuration's measured per-area speed (relative to
-// 256 x 192 at the DiT shapes: 256 x 256 1.06, 384 x 192 1.045; both load
-// 15% fewer bytes per MFMA operation than 256 x 192).  192-token tiles cut
+// 256 x 192, the mean over the DiT's QKV / out / FFN-up / FFN-down GEMMs at
+// M = 11712 and 19904: 256 x 256 1.10, 384 x 192 1.09; both load 15% fewer
+// bytes per MFMA operation than 256 x 192; with these factors the choice is
+// the fastest measured, or within 1% of it, at all eight).  192-token tiles cut
 // M = 11712 exactly; 384 x 192 tiles fill the N = 3072 GEMMs in 2 rounds of
 // 488 tiles (95%), where 256 x 256 makes 552 tiles (3 rounds, 72% full).
 static int default_tile(int64_t M, int64_t N) {
@@ -39,7 +41,7 @@ static int default_tile(int64_t M, int64_t N) {
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         return static_cast<double>((tiles + cus - 1) / cus) * static_cast<double>(bn * bm) / speed;
     };
-    const double c0 = cost(256, 192, 1.0), c1 = cost(256, 256, 1.06), c2 = cost(384, 192, 1.045);
+    const double c0 = cost(256, 192, 1.0), c1 = cost(256, 256, 1.10), c2 = cost(384, 192, 1.09);
     if (c1 < c0 && c1 <= c2) return W8A8_GEMM_TILE_256x256;
     if (c2 < c0) return W8A8_GEMM_TILE_384x192;
     return W8A8_GEMM_TILE_256x192;

@@ -449,8 +449,11 @@ __device__ __forceinline__ void lds_barrier() {
 // [p * W / PASSES, (p + 1) * W / PASSES), W the block's waves) dequantize
 // their accumulators and write them as rows of BN 16-bit values, the 16-byte
 // chunk index XOR-swizzled by the row; then every thread reads whole rows
-// back, 16 bytes per lane, and stores them, so each output line is written
-// whole (N % 8 == 0, out 16-byte aligned).  For MFMA tile (i, j) a lane holds
+// back, 16 bytes per lane, applies GELU (the VALU-heavy part, so that all
+// waves share it rather than the pass's half) and stores them, so each output
+// line is written whole (N % 8 == 0, out 16-byte aligned).  GELU of the
+// rounded linear output is the reference's order (gelu(T(lin)), rounded
+// again).  For MFMA tile (i, j) a lane holds
 // token m = wave_m + 32 j + lane % 32 and channels n = wave_n + 32 i + 8 g +
 // 4 (lane / 32) + {0..3} in acc[i][j][4g .. 4g+3]; the values equal
 // store_tiles'.  Scales come from the side area when it is in use (written
@@ -498,45 +501,46 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
                     xsv[j] = xs[m < M ? m : M - 1];
                 }
             });
-            static_for<0, TN>([&](auto i) {
-                static_for<0, 4>([&](auto g) {
-                    const int chunk = (wave_n + i * 32 + 8 * g) / 8;
-                    const int nl = wave_n + i * 32 + 8 * g + 4 * half;
-                    const int n0 = n_base + nl;
-                    float wsv[4], bv[4];
-                    if constexpr (Side::kUse) {
-                        const float4 w4 = *reinterpret_cast<const float4*>(sv + BM + nl);
-                        const float4 b4 = *reinterpret_cast<const float4*>(sb + nl);
-                        wsv[0] = w4.x; wsv[1] = w4.y; wsv[2] = w4.z; wsv[3] = w4.w;
-                        bv[0] = b4.x; bv[1] = b4.y; bv[2] = b4.z; bv[3] = b4.w;
-                    } else {
-                        static_for<0, 4>([&](auto e) {
-                            const int n = n0 + e < N ? n0 + e : N - 1;
-                            wsv[e] = ws[ws_size == 1 ? 0 : n];
-                            bv[e] = bias ? DType<ODT>::load(static_cast<const OS*>(bias)[n]) : 0.0f;
-                        });
-                    }
-                    static_for<0, TM>([&](auto j) {
-                        float v[4];
-                        uint2 pk;
-                        if constexpr (GELU && ODT == W8A8_BF16) {
-                            // round the pre-activations in pairs, then GELU in pairs
-                            static_for<0, 4>([&](auto e) {
-                                v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], false);
-                            });
-                            pk.x = gelu_bf16x2(pack2_bf16(v[0], v[1]));
-                            pk.y = gelu_bf16x2(pack2_bf16(v[2], v[3]));
-                        } else {
-                            static_for<0, 4>([&](auto e) {
-                                v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], GELU);
-                            });
-                            pk.x = DType<ODT>::store2(v[0], v[1]);
-                            pk.y = DType<ODT>::store2(v[2], v[3]);
-                        }
-                        const int ml = wave_m + j * 32 + lane_m - p * kRows;
-                        *reinterpret_cast<uint2*>(stage + ml * kRowBytes + (chunk ^ out_swz<BN>(ml)) * 16 + half * 8) =
-                            pk;
+            // Channel scales and bias of group k = 4 i + g (channels
+            // wave_n + 32 i + 8 g + 4 half + {0..3}); with the side area the
+            // next group's are read while this group is converted.
+            auto load_group = [&](int k, float4& w4, float4& b4) {
+                const int nl = wave_n + (k / 4) * 32 + 8 * (k % 4) + 4 * half;
+                if constexpr (Side::kUse) {
+                    w4 = *reinterpret_cast<const float4*>(sv + BM + nl);
+                    b4 = *reinterpret_cast<const float4*>(sb + nl);
+                } else {
+                    float wv[4], bv[4];
+                    static_for<0, 4>([&](auto e) {
+                        const int n = n_base + nl + e < N ? n_base + nl + e : N - 1;
+                        wv[e] = ws[ws_size == 1 ? 0 : n];
+                        bv[e] = bias ? DType<ODT>::load(static_cast<const OS*>(bias)[n]) : 0.0f;
                     });
+                    w4 = make_float4(wv[0], wv[1], wv[2], wv[3]);
+                    b4 = make_float4(bv[0], bv[1], bv[2], bv[3]);
+                }
+            };
+            float4 w_next, b_next;
+            load_group(0, w_next, b_next);
+            static_for<0, TN * 4>([&](auto k_) {
+                constexpr int k = decltype(k_)::value, i = k / 4, g = k % 4;
+                const float4 w4 = w_next, b4 = b_next;
+                if constexpr (k + 1 < TN * 4) load_group(k + 1, w_next, b_next);
+                const float wsv[4] = {w4.x, w4.y, w4.z, w4.w};
+                const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+                const int chunk = (wave_n + i * 32 + 8 * g) / 8;
+                static_for<0, TM>([&](auto j) {
+                    // the linear outputs rounded to the output dtype; GELU is
+                    // applied to them in the write-out below
+                    float v[4];
+                    static_for<0, 4>([&](auto e) {
+                        v[e] = epilogue_value<ODT>(acc[i][j][4 * g + e], xsv[j], wsv[e], bv[e], false);
+                    });
+                    uint2 pk;
+                    pk.x = DType<ODT>::store2(v[0], v[1]);
+                    pk.y = DType<ODT>::store2(v[2], v[3]);
+                    const int ml = wave_m + j * 32 + lane_m - p * kRows;
+                    *reinterpret_cast<uint2*>(stage + ml * kRowBytes + (chunk ^ out_swz<BN>(ml)) * 16 + half * 8) = pk;
                 });
             });
         }
@@ -549,6 +553,14 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
             const int m = m_base + p * kRows + r, n = n_base + c * 8;
             uint4 v = *reinterpret_cast<const uint4*>(stage + r * kRowBytes + (c ^ out_swz<BN>(r)) * 16);
             if (m < M && n < N) {
+                if constexpr (GELU) {
+                    // every thread of the block takes part here (in the
+                    // conversion above only the waves of the pass do)
+                    v.x = gelu_x2<ODT>(v.x);
+                    v.y = gelu_x2<ODT>(v.y);
+                    v.z = gelu_x2<ODT>(v.z);
+                    v.w = gelu_x2<ODT>(v.w);
+                }
                 if constexpr (MODE == 2) {
                     const uint4 rv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.resid) +
                                                                      static_cast<int64_t>(m) * N + n);
@@ -580,12 +592,15 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
 // outputs staged through LDS for whole-line stores; kPersist = the kernel
 // loops over output tiles (grid = min(tiles, CUs)) and overlaps each
 // epilogue with the next tile's first loads, which needs a 2-stage ring whose
-// stage holds half of the output tile.
+// stage holds half of the output tile, and accumulators of at most 8 MFMA
+// tiles (128 VGPRs): the tile loop's own live state then fits beside them,
+// while with 3 x 3 tiles (384 x 192) it spilled and measured ~3% slower than
+// one block per tile.
 template <class C, int ODT, int MODE>
 struct DmaPlan {
     static constexpr bool kStaged = MODE != 1 && ODT != W8A8_F32 && C::kStageOut;
-    static constexpr bool kPersist =
-        kStaged && C::STAGES == 2 && C::BN * C::BM <= C::kTileBytes && (C::BM / C::WM) % 2 == 0;
+    static constexpr bool kPersist = kStaged && C::STAGES == 2 && C::BN * C::BM <= C::kTileBytes &&
+                                     (C::BM / C::WM) % 2 == 0 && C::TN * C::TM <= 8;
 };
 
 // Persistent INT8 GEMM over LDS-DMA K tiles.  Block b takes output tiles b,
