@@ -8,7 +8,8 @@
 // Layout of the work: each block stages the M activation rows in LDS and every
 // wave copies its chunks into registers (K <= 64 lanes * XC chunks * 16 B),
 // then walks output channels RPW at a time with a grid stride, streaming each
-// weight row once with 128-bit loads (all chunks of a row in flight at once)
+// weight row once with 128-bit non-temporal loads (all chunks of a row in
+// flight at once)
 // and v_dot4_i32_i8 (sdot4), reducing the per-lane partial dot products with a
 // wave64 butterfly.  Larger K re-reads the activation chunks from L1 instead
 // of holding them.  K % 16 != 0 or unaligned operands take the generic kernel
@@ -66,7 +67,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_vec(const int8_t* __restric
 #pragma unroll
             for (int j = 0; j < (XC > 0 ? XC : 1); ++j) {
                 const int64_t c = lane + j * kWave;
-                wv[r][j] = reinterpret_cast<const uint4*>(w + n * K)[c < nchunks ? c : 0];
+                wv[r][j] = load_stream(reinterpret_cast<const uint4*>(w + n * K) + (c < nchunks ? c : 0));
             }
         }
     };

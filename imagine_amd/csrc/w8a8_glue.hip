@@ -134,7 +134,7 @@ __global__ __launch_bounds__(NT) void adaln_rows_vec(const void* __restrict__ x,
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int64_t c = tid + static_cast<int64_t>(j) * NT;
-        raw[j] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
+        raw[j] = c < nchunks ? load_stream(xr + c) : make_uint4(0, 0, 0, 0);
     }
     auto elem = [&](const uint4& v, int i) {
         return D::load(reinterpret_cast<const typename D::storage*>(&v)[i]);
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(NT) void modnorm_quant_rows_vec(
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int64_t c = tid + static_cast<int64_t>(j) * NT;
-        raw[j] = c < nchunks ? xr[c] : make_uint4(0, 0, 0, 0);
+        raw[j] = c < nchunks ? load_stream(xr + c) : make_uint4(0, 0, 0, 0);
     }
     auto elem = [&](const uint4& v, int i) { return D::load(reinterpret_cast<const OS*>(&v)[i]); };
     const float inv_d = 1.0f / static_cast<float>(d);
@@ -489,7 +489,7 @@ __global__ __launch_bounds__(256) void rms_rope_tokens_vec(const void* q, const 
         for (int g = 0; g < kGroup; ++g) {
             const int64_t h = h0 + g * kRows + sub;
             uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (h < heads) u = *reinterpret_cast<const uint4*>(x + h * d);
+            if (h < heads) u = load_stream(x + h * d);
             const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
             sum[g] = 0.0f;
 #pragma unroll
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(kGlueThreads) void gated_residual_vec(const uint4* 
          c += static_cast<int64_t>(gridDim.x) * kGlueThreads) {
         const int64_t row = c / dc, k = c % dc;
         const int64_t b = row / tokens, t = row % tokens;
-        const uint4 xv = x[c], yv = y[c], gv = (t < prefix ? gate0 : gate1)[b * dc + k];
+        const uint4 xv = load_stream(x + c), yv = load_stream(y + c), gv = (t < prefix ? gate0 : gate1)[b * dc + k];
         const typename D::storage* xe = reinterpret_cast<const typename D::storage*>(&xv);
         const typename D::storage* ye = reinterpret_cast<const typename D::storage*>(&yv);
         const typename D::storage* ge = reinterpret_cast<const typename D::storage*>(&gv);

@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void quant_rows_vec(const void* __restrict__ x
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int64_t c = tid + static_cast<int64_t>(j) * kWave * W;
-            raw[r][j] = (row_ok && c < nchunks) ? src[c] : make_uint4(0, 0, 0, 0);
+            raw[r][j] = (row_ok && c < nchunks) ? load_stream(src + c) : make_uint4(0, 0, 0, 0);
         }
     }
     auto elem = [&](int r, int j, int i) {
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void quant_rows_stream(const void* __restrict_
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int64_t c = tid + static_cast<int64_t>(j) * kWave * W;
-            raw[j] = (ok && c < nchunks) ? src[c] : make_uint4(0, 0, 0, 0);
+            raw[j] = (ok && c < nchunks) ? load_stream(src + c) : make_uint4(0, 0, 0, 0);
         }
     };
     uint4 cur[CPL], nxt[CPL];
