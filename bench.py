@@ -6,7 +6,10 @@ set at 1600x896 with CFG, M = 2 x (5600 + 256) = 11712 tokens, hidden 3072:
   quantize -> FFN-up GEMM (N=12288, GELU-tanh fused epilogue),
   quantize -> FFN-down GEMM (K=12288, N=3072).
 Synthetic seeded inputs (bf16 N(0,1) activations, int8 U[-127,127] weights,
-fp32 per-channel scales U(1e-3,1e-2), bf16 bias N(0,0.02)), resident in HBM.
+fp32 per-channel scales U(1e-3,1e-2), bf16 bias N(0,0.02)), resident in HBM;
+4 sets of the step's three inputs rotate from step to step (864 MB, beyond the
+256 MB Infinity Cache).  After the timed steps the last step's FFN outputs are
+checked on sampled rows against a float64 recomputation ("output_check").
 value = GEMM TOPS of the whole step (2*M*N*K summed over the 4 linears,
 divided by the step time, quantization included in the time).  The default
 50 warmup steps cover the clock settling of a loaded MI355X: measured step
@@ -39,6 +42,7 @@ PEAK_INT8_TOPS = 5000.0       # MI355X dense INT8 MFMA, TOPS
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E, GB/s
 M_TOK = 2 * (5600 + 256)      # 11712
 HID, FFN, QKV = 3072, 12288, 9216
+N_SETS = 4                    # rotating input sets of the step
 LINEARS = [("qkv", HID, QKV, False), ("out", HID, HID, False), ("up", HID, FFN, True),
            ("down", FFN, HID, False)]  # (name, K, N, gelu epilogue)
 
@@ -224,9 +228,11 @@ def main():
     for i, (name, k, n, gelu) in enumerate(LINEARS):
         w, ws, b = make_linear(k, n, 10 + i, dev)
         layers.append((name, k, n, gelu, w, ws, b))
-    x_qkv = torch.randn(M_TOK, HID, generator=gen(1)).to(torch.bfloat16).to(dev)
-    x_out = torch.randn(M_TOK, HID, generator=gen(2)).to(torch.bfloat16).to(dev)
-    x_ffn = torch.randn(M_TOK, HID, generator=gen(3)).to(torch.bfloat16).to(dev)
+    # N_SETS input sets (3 x 72 MB each) rotate from step to step, so the
+    # quantizers read their rows from HBM, not from the 256 MB Infinity Cache.
+    xsets = [[torch.randn(M_TOK, HID, device=dev, generator=torch.Generator(device=dev).manual_seed(3 * i + j + 1))
+              .to(torch.bfloat16) for j in range(3)] for i in range(N_SETS)]
+    x_qkv, _, x_ffn = xsets[0]
     qbuf = {k: torch.empty((M_TOK, k), dtype=torch.int8, device=dev) for k in (HID, FFN)}
     sbuf = torch.empty((M_TOK, 1), dtype=torch.float32, device=dev)
     outs = {name: torch.empty((M_TOK, n), dtype=torch.bfloat16, device=dev) for name, _, n, *_ in layers}
@@ -245,10 +251,14 @@ def main():
 
     up_timer = Timer()
 
+    nstep = [0]
+
     def step(timed=False):
-        quant(x_qkv, qbuf[HID]); gemm(qbuf[HID], layers[0], outs["qkv"], False)
-        quant(x_out, qbuf[HID]); gemm(qbuf[HID], layers[1], outs["out"], False)
-        quant(x_ffn, qbuf[HID])
+        xq, xo, xf = xsets[nstep[0] % N_SETS]
+        nstep[0] += 1
+        quant(xq, qbuf[HID]); gemm(qbuf[HID], layers[0], outs["qkv"], False)
+        quant(xo, qbuf[HID]); gemm(qbuf[HID], layers[1], outs["out"], False)
+        quant(xf, qbuf[HID])
         s = up_timer.start() if timed else None
         gemm(qbuf[HID], layers[2], outs["up"], True)
         if timed:
@@ -279,6 +289,9 @@ def main():
     print(f"[bench] step {ms_per_step:.3f} ms -> {value:.1f} TOPS; up GEMM {up_ms*1e3:.1f} us "
           f"-> {up_tops:.1f} TOPS", file=sys.stderr, flush=True)
 
+    check = validate_step(layers, xsets[(nstep[0] - 1) % N_SETS][2], qbuf, sbuf, outs)
+    print(f"[bench] outputs of the last timed step: {check}", file=sys.stderr, flush=True)
+
     extras = measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv)
     if not args.no_dit_step:
         extras["dit_step_60_blocks_M19904"] = measure_dit_step(W, dev)
@@ -298,9 +311,36 @@ def main():
                      "unit": "TOPS", "frac": round(up_tops / PEAK_INT8_TOPS, 4), "traffic": traffic_bytes(),
                      "launch_us": round(up_ms * 1e3, 2), "algorithmic_ops": up_ops},
         "cpu_baseline": cpu,
+        "output_check": check,
         "extras": extras,
     }
     print(json.dumps(line), flush=True)
+
+
+def validate_step(layers, x_ffn, qbuf, sbuf, outs, nrows=8):
+    """Sanity check of the last timed step's FFN outputs (sampled rows) against
+    a float64 torch recomputation from the int8 codes those GEMMs consumed:
+    FFN-up from the codes of x_ffn (its per-token scales amax/127 recomputed
+    from x_ffn), FFN-down from the codes and scales of the FFN-up output.  Not
+    the parity tests (those hold every value bit for bit against the oracle);
+    the bound is the north star's max relative error 1e-2."""
+    rows = torch.linspace(0, M_TOK - 1, nrows, device=x_ffn.device).long()
+    _, _, _, _, w_up, ws_up, b_up = layers[2]
+    _, _, _, _, w_dn, ws_dn, b_dn = layers[3]
+    xf = x_ffn[rows].double()
+    s_in = (xf.abs().amax(dim=1).float() / 127.0).clamp_min(1e-30).double()
+    acc_up = qbuf[HID][rows].double() @ w_up.double().t()
+    lin = acc_up * s_in[:, None] * ws_up.double() + b_up.double()
+    up_ref = 0.5 * lin * (1.0 + torch.tanh(0.7978845608028654 * (lin + 0.044715 * lin ** 3)))
+    acc_dn = qbuf[FFN][rows].double() @ w_dn.double().t()
+    dn_ref = acc_dn * sbuf[rows].double() * ws_dn.double() + b_dn.double()
+
+    def rel(out, ref):
+        return float(((out.double() - ref).abs().amax(dim=1) / ref.abs().amax(dim=1)).max())
+
+    e_up, e_dn = rel(outs["up"][rows], up_ref), rel(outs["down"][rows], dn_ref)
+    return {"rows": nrows, "ffn_up_max_rel_err": round(e_up, 6), "ffn_down_max_rel_err": round(e_dn, 6),
+            "ok": e_up <= 1e-2 and e_dn <= 1e-2}
 
 
 def traffic_bytes():
