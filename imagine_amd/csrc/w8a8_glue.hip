@@ -130,11 +130,20 @@ __global__ __launch_bounds__(NT) void adaln_rows_vec(const void* __restrict__ x,
     const uint4* sr = reinterpret_cast<const uint4*>(static_cast<const char*>(scale) + (row / sg) * d * D::bytes);
     const uint4* hr = reinterpret_cast<const uint4*>(static_cast<const char*>(shift) + (row / tg) * d * D::bytes);
     uint4* o = reinterpret_cast<uint4*>(static_cast<char*>(out) + row * d * D::bytes);
-    uint4 raw[CPL];
+    // the row and, for rows of up to 3 chunks per thread (64 VGPRs: full
+    // occupancy), its scale and shift chunks, loaded now so that their
+    // latency is not a second round trip after the row reductions
+    // (2 x 5856 x 3072 bf16: ~5% faster)
+    constexpr int PF = CPL <= 3 ? CPL : 1;
+    uint4 raw[CPL], svp[PF], hvp[PF];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int64_t c = tid + static_cast<int64_t>(j) * NT;
         raw[j] = c < nchunks ? load_stream(xr + c) : make_uint4(0, 0, 0, 0);
+        if constexpr (CPL <= 3) {
+            svp[j] = c < nchunks ? sr[c] : make_uint4(0, 0, 0, 0);
+            hvp[j] = c < nchunks ? hr[c] : make_uint4(0, 0, 0, 0);
+        }
     }
     auto elem = [&](const uint4& v, int i) {
         return D::load(reinterpret_cast<const typename D::storage*>(&v)[i]);
@@ -178,7 +187,14 @@ __global__ __launch_bounds__(NT) void adaln_rows_vec(const void* __restrict__ x,
     for (int j = 0; j < CPL; ++j) {
         const int64_t c = tid + static_cast<int64_t>(j) * NT;
         if (c >= nchunks) break;
-        const uint4 sv = sr[c], hv = hr[c];
+        uint4 sv, hv;
+        if constexpr (CPL <= 3) {
+            sv = svp[j];
+            hv = hvp[j];
+        } else {
+            sv = sr[c];
+            hv = hr[c];
+        }
         uint4 res;
         typename D::storage* rp = reinterpret_cast<typename D::storage*>(&res);
 #pragma unroll
