@@ -31,7 +31,10 @@ constexpr int kWave = 64;
 // Outputs keep ordinary stores: the next kernel reads them (codes, normalised
 // rows), and non-temporal stores there made the block linear set 0.5% and
 // the DiT step's W8A8 linears 1.5% slower although the kernels that wrote
-// them got faster.
+// them got faster.  Only for loads whose wave covers whole lines at once: in
+// the ConvRot quantizer, where each lane reads its own 128-byte span 16 bytes
+// per instruction, it made the kernel 35% slower (lines evicted between the
+// instructions that share them).
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint4 load_stream(const void* p) {

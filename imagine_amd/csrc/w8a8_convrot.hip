@@ -60,24 +60,45 @@ __device__ __forceinline__ void h4_sum(float& a, float& b, float& c, float& d) {
     d = (x2 - m) + x3;
 }
 
-// Value of v in lane K of this lane's quad (DPP quad_perm [K,K,K,K]; every
-// lane is active wherever this is used, so no source lane is ever invalid).
-// bound_ctrl lets the compiler fold the move into the consuming mul / fmac.
-template <int K>
-__device__ __forceinline__ float quad_lane(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xf, 0xf, true));
+// Stage across the quad, four values a, b, c, d at once: lane d of the quad
+// gets (H4 row d) . (x0..x3), x_k being the value of quad lane k; sg[k] is -1
+// where row d of H4 has its minus sign (k == 3 - d), else +1.  One DPP
+// instruction per term: v_mul_f32_dpp for x0 * sg0, then v_fmac_f32_dpp
+// t += x_k * sg_k (exact products, so each is the reference's t +- x_k,
+// rounded once).  Written with builtins, the compiler folds the quad
+// broadcast into the multiply but not into the fmac (7 instructions per value
+// instead of 4), so the block is written out; the
+// four chains are interleaved, and s_nop 4 first gives the wait states a DPP
+// read needs after a VALU write of its source (and after an EXEC write).
+// All lanes of every quad are active wherever this is used.
+#define W8A8_DPP_Q(K) "quad_perm:[" #K "," #K "," #K "," #K "] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+__device__ __forceinline__ void h4_across_quad_x4(float& a, float& b, float& c, float& d, const float (&sg)[4]) {
+    float ta, tb, tc, td;
+    asm("s_nop 4\n\t"
+        "v_mul_f32_dpp %0, %4, %8 " W8A8_DPP_Q(0)
+        "v_mul_f32_dpp %1, %5, %8 " W8A8_DPP_Q(0)
+        "v_mul_f32_dpp %2, %6, %8 " W8A8_DPP_Q(0)
+        "v_mul_f32_dpp %3, %7, %8 " W8A8_DPP_Q(0)
+        "v_fmac_f32_dpp %0, %4, %9 " W8A8_DPP_Q(1)
+        "v_fmac_f32_dpp %1, %5, %9 " W8A8_DPP_Q(1)
+        "v_fmac_f32_dpp %2, %6, %9 " W8A8_DPP_Q(1)
+        "v_fmac_f32_dpp %3, %7, %9 " W8A8_DPP_Q(1)
+        "v_fmac_f32_dpp %0, %4, %10 " W8A8_DPP_Q(2)
+        "v_fmac_f32_dpp %1, %5, %10 " W8A8_DPP_Q(2)
+        "v_fmac_f32_dpp %2, %6, %10 " W8A8_DPP_Q(2)
+        "v_fmac_f32_dpp %3, %7, %10 " W8A8_DPP_Q(2)
+        "v_fmac_f32_dpp %0, %4, %11 " W8A8_DPP_Q(3)
+        "v_fmac_f32_dpp %1, %5, %11 " W8A8_DPP_Q(3)
+        "v_fmac_f32_dpp %2, %6, %11 " W8A8_DPP_Q(3)
+        "v_fmac_f32_dpp %3, %7, %11 quad_perm:[3,3,3,3] row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=&v"(ta), "=&v"(tb), "=&v"(tc), "=&v"(td)
+        : "v"(a), "v"(b), "v"(c), "v"(d), "v"(sg[0]), "v"(sg[1]), "v"(sg[2]), "v"(sg[3]));
+    a = ta;
+    b = tb;
+    c = tc;
+    d = td;
 }
-
-// Stage across the quad: lane d of the quad gets (H4 row d) . (x0..x3), x_k
-// being v of quad lane k.  sg[k] is -1 where row d of H4 has its minus sign
-// (k == 3 - d), else +1; the products are exact, so fma(x, sg, t) is the
-// reference's t +- x.
-__device__ __forceinline__ float h4_sum_across_quad(float v, const float (&sg)[4]) {
-    float t = quad_lane<0>(v) * sg[0];
-    t = fmaf(quad_lane<1>(v), sg[1], t);
-    t = fmaf(quad_lane<2>(v), sg[2], t);
-    return fmaf(quad_lane<3>(v), sg[3], t);
-}
+#undef W8A8_DPP_Q
 
 // The in-register stages of a lane's 64 elements: strides 1, 4, 16, as many
 // as the group has (G = 4, 16, 64 or more), unscaled.
@@ -144,9 +165,10 @@ __global__ __launch_bounds__(1024) void convrot_quant_rows(const void* __restric
     for (int k = 0; k < 4; ++k) sg[k] = (k == 3 - d3) ? -1.0f : 1.0f;
     float m = 0.0f;
 #pragma unroll
-    for (int r = 0; r < kLaneElems; ++r) {
-        v[r] = h4_sum_across_quad(v[r], sg);  // 16 y
-        m = fmaxf(m, fabsf(v[r]));
+    for (int r = 0; r < kLaneElems; r += 4) {
+        h4_across_quad_x4(v[r], v[r + 1], v[r + 2], v[r + 3], sg);  // 16 y
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(v[r + i]));
     }
     // quad max: quad_perm [1,0,3,2] then [2,3,0,1]
     m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0xb1, 0xf, 0xf, false)));
@@ -268,11 +290,13 @@ __global__ __launch_bounds__(256) void convrot_rotate_vec(const void* __restrict
     constexpr float kScale = G == 4 ? 0.5f : G == 16 ? 0.25f : G == 64 ? 0.125f : 0.0625f;
 #pragma unroll
     for (int k = 0; k < kLaneElems / E; ++k) {
+        if constexpr (G == kRotGroup) {
 #pragma unroll
-        for (int i = 0; i < E; ++i) {
-            if constexpr (G == kRotGroup) v[k * E + i] = h4_sum_across_quad(v[k * E + i], sg);
-            v[k * E + i] *= kScale;
+            for (int i = 0; i < E; i += 4)
+                h4_across_quad_x4(v[k * E + i], v[k * E + i + 1], v[k * E + i + 2], v[k * E + i + 3], sg);
         }
+#pragma unroll
+        for (int i = 0; i < E; ++i) v[k * E + i] *= kScale;
         uint4 out;
         uint32_t* w = reinterpret_cast<uint32_t*>(&out);
 #pragma unroll
