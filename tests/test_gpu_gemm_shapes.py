@@ -101,6 +101,42 @@ def test_every_main_loop_bit_exact(tile, mode, shape):
     assert np.array_equal(storage(got, odt), want)
 
 
+PERSIST_MODES = ["bf16", "bf16_gelu", "f16", "f16_gelu", "bf16_residual", "f16_residual"]
+
+
+@pytest.mark.parametrize("mode", PERSIST_MODES)
+@pytest.mark.parametrize("tile", [L.TILE_256x256, L.TILE_256x192], ids=lambda t: L.TILE_NAMES[t])
+def test_persistent_tile_loop_bit_exact(tile, mode):
+    """The main loops that loop over output tiles (one block per CU), on a
+    shape with more tiles than the GPU has CUs (306 and 396 tiles; ragged
+    last tiles in M and N), so blocks take a second tile after their first
+    epilogue: every output mode, 48 sampled rows (all columns) against the
+    oracle."""
+    m, n, k = 4100, 4392, 256
+    assert W.gemm_config(m, n, k, tile) == L.TILE_NAMES[tile]
+    odt = mode.split("_")[0]
+    x = dev_x(m, k, seed=31, scale=1.5)
+    w = dev_w(n, k, seed=32)
+    ws = dev_scales(n, seed=33)
+    bias = (torch.randn(n, device=DEV, generator=dev_gen(34)) * 0.5).to(TD[odt])
+    q, xs = W.quantize_rowwise(x)
+    rows = sample_rows(m, 48, seed=35)
+    qh, xsh = q[rows].cpu().numpy(), xs.cpu().numpy().reshape(-1)[rows]
+    acc = O.gemm_i32(qh, w.cpu().numpy())
+    if mode.endswith("_residual"):
+        g = dev_gen(36)
+        resid = (torch.randn(m, n, device=DEV, generator=g) * 2).to(TD[odt])
+        rscale = (torch.rand(n, device=DEV, generator=g) + 0.25).to(TD[odt])
+        got = W.gemm_dequant_residual(q, w, xs, ws, bias, TD[odt], resid, rscale, tile=tile)
+        lin = O.epilogue_kitchen(acc, xsh, ws.cpu().numpy(), storage(bias, odt), odt)
+        want = O.residual(lin, storage(resid[rows], odt), storage(rscale, odt), odt)
+    else:
+        gelu = mode.endswith("_gelu")
+        got = W.gemm_dequant(q, w, xs, ws, bias, TD[odt], gelu=gelu, tile=tile)
+        want = O.epilogue_kitchen(acc, xsh, ws.cpu().numpy(), storage(bias, odt), odt, act=1 if gelu else 0)
+    assert np.array_equal(storage(got[rows], odt), want)
+
+
 def test_requested_tile_falls_back_when_k_does_not_fit():
     """A 128-byte-K-tile main loop requested for K = 192 runs the 64-byte one;
     K = 48 runs the register-staged loop; K = 13 the generic kernel."""
