@@ -474,11 +474,20 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
                                                    const Residual& res, void* __restrict__ out,
                                                    Hook before_store) {
     constexpr int BN = C::BN, BM = C::BM, TN = C::TN, TM = C::TM;
-    constexpr int kRowBytes = BN * 2;
-    constexpr int kChunks = BN / 8;   // 16-byte chunks per staged row
-    constexpr int kRows = BM / PASSES;
+    // The passes split the tile by channels when every wave's channel
+    // columns split into whole 128-byte line segments (256 x 256 tiles: two
+    // passes of 64 channels per wave column): then all waves convert in each
+    // pass, two per SIMD.  Otherwise they split it by rows, and only the
+    // waves holding a pass's rows convert in it.
+    constexpr bool kSplitN = PASSES > 1 && TN % PASSES == 0 && (C::WN / PASSES) % 64 == 0;
+    constexpr int kPassCols = kSplitN ? BN / PASSES : BN;   // channels per staged row
+    constexpr int kSegCols = kSplitN ? C::WN / PASSES : BN;  // contiguous channels of a segment
+    constexpr int kTnPass = kSplitN ? TN / PASSES : TN;     // MFMA column tiles per pass
+    constexpr int kRowBytes = kPassCols * 2;
+    constexpr int kChunks = kPassCols / 8;   // 16-byte chunks per staged row
+    constexpr int kRows = kSplitN ? BM : BM / PASSES;
     constexpr int kWavesPerPass = C::kWaves / PASSES;
-    static_assert((BM / C::WM) % PASSES == 0, "each pass holds whole wave rows");
+    static_assert(kSplitN || (BM / C::WM) % PASSES == 0, "each pass holds whole wave rows");
     static_assert(kRows * kChunks % C::kThreads == 0, "whole write-out passes over the block");
     using OS = typename DType<ODT>::storage;
     // Lane-derived addresses are recomputed here from values the compiler
@@ -491,7 +500,7 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
     const float* const sb = sv + BM + BN;                                      // [BN bias]
     static_for<0, PASSES>([&](auto p_) {
         constexpr int p = decltype(p_)::value;
-        if (wave / kWavesPerPass == p) {   // wave-uniform
+        if (kSplitN || wave / kWavesPerPass == p) {   // wave-uniform
             float xsv[TM];
             static_for<0, TM>([&](auto j) {
                 if constexpr (Side::kUse) {
@@ -520,15 +529,18 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
                     b4 = make_float4(bv[0], bv[1], bv[2], bv[3]);
                 }
             };
+            // the pass's column tiles: i in [i0, i0 + kTnPass)
+            constexpr int i0 = kSplitN ? p * kTnPass : 0;
             float4 w_next, b_next;
-            load_group(0, w_next, b_next);
-            static_for<0, TN * 4>([&](auto k_) {
-                constexpr int k = decltype(k_)::value, i = k / 4, g = k % 4;
+            load_group(4 * i0, w_next, b_next);
+            static_for<0, kTnPass * 4>([&](auto k_) {
+                constexpr int k = 4 * i0 + decltype(k_)::value, i = k / 4, g = k % 4;
                 const float4 w4 = w_next, b4 = b_next;
-                if constexpr (k + 1 < TN * 4) load_group(k + 1, w_next, b_next);
+                if constexpr (k + 1 < 4 * (i0 + kTnPass)) load_group(k + 1, w_next, b_next);
                 const float wsv[4] = {w4.x, w4.y, w4.z, w4.w};
                 const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
-                const int chunk = (wave_n + i * 32 + 8 * g) / 8;
+                const int chunk = kSplitN ? ((wave_n / C::WN) * kSegCols + (i - i0) * 32 + 8 * g) / 8
+                                          : (wave_n + i * 32 + 8 * g) / 8;
                 static_for<0, TM>([&](auto j) {
                     // the linear outputs rounded to the output dtype; GELU is
                     // applied to them in the write-out below
@@ -539,8 +551,9 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
                     uint2 pk;
                     pk.x = DType<ODT>::store2(v[0], v[1]);
                     pk.y = DType<ODT>::store2(v[2], v[3]);
-                    const int ml = wave_m + j * 32 + lane_m - p * kRows;
-                    *reinterpret_cast<uint2*>(stage + ml * kRowBytes + (chunk ^ out_swz<BN>(ml)) * 16 + half * 8) = pk;
+                    const int ml = wave_m + j * 32 + lane_m - (kSplitN ? 0 : p * kRows);
+                    *reinterpret_cast<uint2*>(stage + ml * kRowBytes + (chunk ^ out_swz<kPassCols>(ml)) * 16 +
+                                              half * 8) = pk;
                 });
             });
         }
@@ -550,8 +563,10 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
         for (int pass = 0; pass < kRows * kChunks / C::kThreads; ++pass) {
             const int idx = pass * C::kThreads + tv;
             const int r = idx / kChunks, c = idx % kChunks;
-            const int m = m_base + p * kRows + r, n = n_base + c * 8;
-            uint4 v = *reinterpret_cast<const uint4*>(stage + r * kRowBytes + (c ^ out_swz<BN>(r)) * 16);
+            const int m = m_base + (kSplitN ? 0 : p * kRows) + r;
+            const int n = kSplitN ? n_base + (c / (kSegCols / 8)) * C::WN + p * kSegCols + (c % (kSegCols / 8)) * 8
+                                  : n_base + c * 8;
+            uint4 v = *reinterpret_cast<const uint4*>(stage + r * kRowBytes + (c ^ out_swz<kPassCols>(r)) * 16);
             if (m < M && n < N) {
                 if constexpr (GELU) {
                     // every thread of the block takes part here (in the
