@@ -559,13 +559,32 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
         }
         lds_barrier();
         if constexpr (p == 0) before_store();
+        // Thread tv takes chunk c = tv % kChunks of rows r0, r0 + kRowStep, ...
+        // (r0 = tv / kChunks) when the block covers whole rows per step, so
+        // the column, the bounds check on it and the row addresses are set up
+        // once per pass and stepped; otherwise each chunk index is decoded.
+        constexpr bool kWholeRows = C::kThreads % kChunks == 0;
+        constexpr int kRowStep = kWholeRows ? C::kThreads / kChunks : 1;
+        const int c0 = tv % kChunks, r0 = tv / kChunks;
+        const int n0 = kSplitN ? n_base + (c0 / (kSegCols / 8)) * C::WN + p * kSegCols + (c0 % (kSegCols / 8)) * 8
+                               : n_base + c0 * 8;
+        const int m0 = m_base + (kSplitN ? 0 : p * kRows) + r0;
 #pragma unroll 4
         for (int pass = 0; pass < kRows * kChunks / C::kThreads; ++pass) {
-            const int idx = pass * C::kThreads + tv;
-            const int r = idx / kChunks, c = idx % kChunks;
-            const int m = m_base + (kSplitN ? 0 : p * kRows) + r;
-            const int n = kSplitN ? n_base + (c / (kSegCols / 8)) * C::WN + p * kSegCols + (c % (kSegCols / 8)) * 8
-                                  : n_base + c * 8;
+            int r, c, m, n;
+            if constexpr (kWholeRows) {
+                r = r0 + pass * kRowStep;
+                c = c0;
+                m = m0 + pass * kRowStep;
+                n = n0;
+            } else {
+                const int idx = pass * C::kThreads + tv;
+                r = idx / kChunks;
+                c = idx % kChunks;
+                m = m_base + (kSplitN ? 0 : p * kRows) + r;
+                n = kSplitN ? n_base + (c / (kSegCols / 8)) * C::WN + p * kSegCols + (c % (kSegCols / 8)) * 8
+                            : n_base + c * 8;
+            }
             uint4 v = *reinterpret_cast<const uint4*>(stage + r * kRowBytes + (c ^ out_swz<kPassCols>(r)) * 16);
             if (m < M && n < N) {
                 if constexpr (GELU) {
