@@ -444,14 +444,16 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// Epilogue of 16-bit outputs through an LDS staging area, in PASSES passes
-// of BM / PASSES rows.  In pass p the waves holding those rows (waves
-// [p * W / PASSES, (p + 1) * W / PASSES), W the block's waves) dequantize
-// their accumulators and write them as rows of BN 16-bit values, the 16-byte
-// chunk index XOR-swizzled by the row; then every thread reads whole rows
-// back, 16 bytes per lane, applies GELU (the VALU-heavy part, so that all
-// waves share it rather than the pass's half) and stores them, so each output
-// line is written whole (N % 8 == 0, out 16-byte aligned).  GELU of the
+// Epilogue of 16-bit outputs through an LDS staging area, in PASSES passes,
+// each of half the tile when PASSES = 2: of its channels (kSplitN below: all
+// waves convert the pass's MFMA column tiles) or of its rows (the waves
+// holding those rows, [p * W / PASSES, (p + 1) * W / PASSES) of the block's
+// W waves, convert).  The converted values are written as staged rows of
+// 16-bit values, the 16-byte chunk index XOR-swizzled by the row; then every
+// thread reads staged chunks back, 16 bytes per lane, applies GELU (the
+// VALU-heavy part, shared by all waves) and stores them, so each output
+// line segment of 128 bytes or more is written whole (N % 8 == 0, out
+// 16-byte aligned).  GELU of the
 // rounded linear output is the reference's order (gelu(T(lin)), rounded
 // again).  For MFMA tile (i, j) a lane holds
 // token m = wave_m + 32 j + lane % 32 and channels n = wave_n + 32 i + 8 g +
