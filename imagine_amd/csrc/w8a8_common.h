@@ -146,8 +146,9 @@ template <> struct DType<W8A8_BF16> {
 //                                            x * +0 = -0 as the reference does)
 // exp2 and the reciprocal are the hardware approximations (about 1 ulp); the
 // fp32 result carries a few ulps of error, which bf16 rounding never shows.
-// About 13 VALU slots; it runs in the FFN-up epilogue while the matrix cores
-// idle, where a table lookup measured 12-18% slower on the whole GEMM.
+// About 13 VALU slots, two of them quarter-rate.  The GEMM's staged epilogue
+// looks its results up instead (gelu_bf16x8_lut below, about 4 operations and
+// one LDS read per value).
 __device__ __forceinline__ float gelu_tanh_fast(float x) {
     const float kA = 2.302208198144325f;      // sqrt(2/pi) * 2 / ln 2
     const float kB = 0.1029432395800235f;     // sqrt(2/pi) * 0.044715 * 2 / ln 2
@@ -196,6 +197,69 @@ template <int DT>
 __device__ __forceinline__ uint32_t gelu_x2(uint32_t p) {
     if constexpr (DT == W8A8_BF16) return gelu_bf16x2(p);
     else return gelu_f16_bits(p & 0xffffu) | (gelu_f16_bits(p >> 16) << 16);
+}
+
+// bf16 GELU by lookup in a 16 KB LDS table of gelu_bf16x2's own results, for
+// the VALU-bound epilogue of the GEMM.  Word u of the table holds the GELU of
+// the patterns kGeluLutLo + u (low half) and 0x8000 | (kGeluLutLo + u) (high
+// half): magnitudes 2^-22 up to 2^10 of either sign.  For a pattern b,
+// d = (b - kGeluLutLo) mod 2^16 is in range iff bits 12-14 of d are clear,
+// and its entry's byte offset is then (4 d mod 2^16) | (d >> 14) = 4u + 2s, s
+// the sign: both halves of a word are offset by the same three packed 16-bit
+// operations.  An out-of-range offset is still below 64 KB, so the reads stay
+// inside a block LDS array of at least 64 KB with the table at its start.
+// Filled per block from gelu_bf16x2, the lookup equals gelu_bf16x2 bit for
+// bit wherever it applies.
+constexpr uint32_t kGeluLutLo = 0x3480u;        // bf16 2^-22
+constexpr int kGeluLutBytes = 4096 * 4;
+
+// Fills the table: thread t of nthreads writes words t, t + nthreads, ...
+__device__ __forceinline__ void gelu_lut_fill(int8_t* tab, int t, int nthreads) {
+    for (int u = t; u < kGeluLutBytes / 4; u += nthreads) {
+        const uint32_t b = kGeluLutLo + u;
+        reinterpret_cast<uint32_t*>(tab)[u] = gelu_bf16x2(b | ((b | 0x8000u) << 16));
+    }
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// GELU of 8 bf16 values (a 16-byte chunk): table lookups when all 8 are in the
+// table's range, else gelu_bf16x2 for the whole chunk.  `base` is the table's
+// LDS address; [base, base + 64 KB) lies inside the block's LDS.  All eight
+// lookups are issued before the first result is used, each pair into the two
+// halves of one register.
+__device__ __forceinline__ uint4 gelu_bf16x8_lut(uint4 v, uint32_t base) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(3))) unsigned short* lds_u16;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const u16x2 lo2 = {static_cast<unsigned short>(kGeluLutLo), static_cast<unsigned short>(kGeluLutLo)};
+    uint32_t off[8], miss = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const u16x2 d = __builtin_bit_cast(u16x2, w[k]) - lo2;
+        const uint32_t q = __builtin_bit_cast(uint32_t, static_cast<u16x2>((d << 2) | (d >> 14)));
+        miss |= __builtin_bit_cast(uint32_t, d);
+        off[2 * k] = (q & 0xffffu) | base;
+        off[2 * k + 1] = (q >> 16) | base;
+    }
+    u16x2 g[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        g[k].x = *(lds_u16)static_cast<uintptr_t>(off[2 * k]);
+        g[k].y = *(lds_u16)static_cast<uintptr_t>(off[2 * k + 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t r[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = __builtin_bit_cast(uint32_t, g[k]);
+    if (__builtin_expect((miss & 0x70007000u) != 0, 0)) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = gelu_bf16x2(w[k]);
+    }
+    return make_uint4(r[0], r[1], r[2], r[3]);
 }
 
 // GELU of a value v already rounded to dtype T, as a float.

@@ -421,6 +421,19 @@ struct SideArea {
     static constexpr int kIters = kUse ? (kValues + C::kThreads - 1) / C::kThreads : 1;
 };
 
+// bf16 GELU table of the staged epilogue (gelu_bf16x8_lut) at the start of
+// the block's LDS array, where the LDS has room for it: the ring (and the side
+// area after it) then start at byte kRing.
+template <class C, int ODT, int MODE, bool GELU>
+struct GeluLut {
+    using Side = SideArea<C, ODT, MODE>;
+    static constexpr bool kUse = GELU && ODT == W8A8_BF16 && Side::kUse &&
+                                 kGeluLutBytes + C::kLds + Side::kBytes <= kLdsPerCU;
+    static constexpr int kRing = kUse ? kGeluLutBytes : 0;
+    static constexpr int kArrayBytes = kRing + C::kLds + Side::kBytes;
+    static_assert(!kUse || kArrayBytes >= 65536, "lookups read up to 64 KB past the table's start");
+};
+
 // The 16-byte output chunk c of staged row r sits at chunk c ^ (r mod P), P
 // the largest power of two up to 32 dividing the chunks per row (48 for
 // 384-wide tiles: P = 16), so the swizzled chunk stays inside its row.
@@ -571,25 +584,42 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
         const int n0 = kSplitN ? n_base + (c0 / (kSegCols / 8)) * C::WN + p * kSegCols + (c0 % (kSegCols / 8)) * 8
                                : n_base + c0 * 8;
         const int m0 = m_base + (kSplitN ? 0 : p * kRows) + r0;
-#pragma unroll 4
-        for (int pass = 0; pass < kRows * kChunks / C::kThreads; ++pass) {
-            int r, c, m, n;
+        constexpr int kSteps = kRows * kChunks / C::kThreads;
+        auto coords = [&](int step, int& r, int& c, int& m, int& n) {
             if constexpr (kWholeRows) {
-                r = r0 + pass * kRowStep;
+                r = r0 + step * kRowStep;
                 c = c0;
-                m = m0 + pass * kRowStep;
+                m = m0 + step * kRowStep;
                 n = n0;
             } else {
-                const int idx = pass * C::kThreads + tv;
+                const int idx = step * C::kThreads + tv;
                 r = idx / kChunks;
                 c = idx % kChunks;
                 m = m_base + (kSplitN ? 0 : p * kRows) + r;
                 n = kSplitN ? n_base + (c / (kSegCols / 8)) * C::WN + p * kSegCols + (c % (kSegCols / 8)) * 8
                             : n_base + c * 8;
             }
-            uint4 v = *reinterpret_cast<const uint4*>(stage + r * kRowBytes + (c ^ out_swz<kPassCols>(r)) * 16);
+        };
+        auto staged = [&](int r, int c) {
+            return *reinterpret_cast<const uint4*>(stage + r * kRowBytes + (c ^ out_swz<kPassCols>(r)) * 16);
+        };
+        // each step's staged chunk is read one step ahead (the last step
+        // re-reads its own), so the read's latency hides under the previous
+        // chunk's work
+        int r_nx, c_nx, m_nx, n_nx;   // the next step's chunk
+        coords(0, r_nx, c_nx, m_nx, n_nx);
+        uint4 v_next = staged(r_nx, c_nx);
+#pragma unroll 4
+        for (int step = 0; step < kSteps; ++step) {
+            uint4 v = v_next;
+            const int m = m_nx, n = n_nx;
+            coords(step + 1 < kSteps ? step + 1 : step, r_nx, c_nx, m_nx, n_nx);
+            v_next = staged(r_nx, c_nx);
             if (m < M && n < N) {
-                if constexpr (GELU) {
+                if constexpr (GeluLut<C, ODT, MODE, GELU>::kUse) {
+                    using Lut = GeluLut<C, ODT, MODE, GELU>;
+                    v = gelu_bf16x8_lut(v, lds_address(lds - Lut::kRing));
+                } else if constexpr (GELU) {
                     // every thread of the block takes part here (in the
                     // conversion above only the waves of the pass do)
                     v.x = gelu_x2<ODT>(v.x);
@@ -660,7 +690,9 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
     using Side = SideArea<C, ODT, MODE>;
     constexpr bool kStaged = DmaPlan<C, ODT, MODE>::kStaged;
     constexpr bool kPersist = DmaPlan<C, ODT, MODE>::kPersist;
-    __shared__ __attribute__((aligned(1024))) int8_t lds[C::kLds + Side::kBytes];
+    using Lut = GeluLut<C, ODT, MODE, GELU>;
+    __shared__ __attribute__((aligned(1024))) int8_t lds_all[Lut::kArrayBytes];
+    int8_t* const lds = lds_all + Lut::kRing;   // the ring, then the side area
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN, tiles = tiles_m * tiles_n;
     // The wave index is uniform across the wave: in an SGPR, so operand choice,
@@ -773,6 +805,10 @@ __global__ __launch_bounds__(C::kThreads, C::OCC) void gemm_mfma_dma(
         });
     };
     auto next_stage = [](int st) { return st + 1 == STAGES ? 0 : st + 1; };
+
+    // The GELU table is written once; the barriers of the first K loop order
+    // it before the first epilogue's reads.
+    if constexpr (Lut::kUse) gelu_lut_fill(lds_all, t, C::kThreads);
 
     int s0 = 0;           // ring stage of the current tile's K tile 0
     bool primed = false;  // K tile 0 landed (and waited for) and K tile 1 issued by the previous epilogue

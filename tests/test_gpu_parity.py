@@ -366,7 +366,8 @@ def test_dequantize_linear_bit_exact():
     assert np.array_equal(storage(out, "f16"), want)
 
 
-@pytest.mark.parametrize("tile", [W._lib.TILE_AUTO, W._lib.TILE_256x128, W._lib.TILE_REGS, W._lib.TILE_GENERIC],
+@pytest.mark.parametrize("tile", [W._lib.TILE_AUTO, W._lib.TILE_256x256, W._lib.TILE_256x192, W._lib.TILE_384x192,
+                                  W._lib.TILE_256x128, W._lib.TILE_REGS, W._lib.TILE_GENERIC],
                          ids=lambda t: W._lib.TILE_NAMES[t])
 @pytest.mark.parametrize("odt", ["bf16", "f16"])
 def test_gemm_gelu_epilogue_every_preactivation(odt, tile):
@@ -375,9 +376,10 @@ def test_gemm_gelu_epilogue_every_preactivation(odt, tile):
     fma(0 * xs, ws, bias[n]) = bias[n] exactly; the bias takes every finite bit
     pattern of the output dtype (the saturated tails, the cancelling negative
     tail, subnormals and signed zeros included).  Bit for bit against the
-    oracle, on the staged epilogue of a DMA main loop with one block per CU
-    (auto), of the two-blocks-per-CU one (256x128), and on the register-staged
-    and generic main loops."""
+    oracle, on the staged epilogue of each DMA tile with one block per CU
+    (256x256 and 256x192 look bf16 GELU up in an LDS table for magnitudes
+    2^-22 to 2^10, 384x192 evaluates it), of the two-blocks-per-CU one
+    (256x128), and on the register-staged and generic main loops."""
     bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
     bits = bits[np.isfinite(O.to_f32(bits, odt))]
     n = (len(bits) + 255) // 256 * 256
