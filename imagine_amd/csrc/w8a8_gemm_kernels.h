@@ -462,11 +462,12 @@ __device__ __forceinline__ void lds_barrier() {
 // waves convert the pass's MFMA column tiles) or of its rows (the waves
 // holding those rows, [p * W / PASSES, (p + 1) * W / PASSES) of the block's
 // W waves, convert).  The converted values are written as staged rows of
-// 16-bit values, the 16-byte chunk index XOR-swizzled by the row; then every
-// thread reads staged chunks back, 16 bytes per lane, applies GELU (the
-// VALU-heavy part, shared by all waves) and stores them, so each output
-// line segment of 128 bytes or more is written whole (N % 8 == 0, out
-// 16-byte aligned).  GELU of the
+// 16-bit values, the 16-byte chunk index XOR-swizzled by the row; then
+// threads read staged chunks back, 16 bytes per lane, apply GELU and store
+// them, so each output line segment of 128 bytes or more is written whole
+// (N % 8 == 0, out 16-byte aligned).  When a wave's pass segment is one
+// 128-byte line per row (kWaveLocal), each wave stages and stores its own
+// rows; otherwise the block's threads share the write-out.  GELU of the
 // rounded linear output is the reference's order (gelu(T(lin)), rounded
 // again).  For MFMA tile (i, j) a lane holds
 // token m = wave_m + 32 j + lane % 32 and channels n = wave_n + 32 i + 8 g +
@@ -502,6 +503,13 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
     constexpr int kChunks = kPassCols / 8;   // 16-byte chunks per staged row
     constexpr int kRows = kSplitN ? BM : BM / PASSES;
     constexpr int kWavesPerPass = C::kWaves / PASSES;
+    // With kWaveLocal each wave stages its own WM rows of the pass's
+    // 64-channel segment (128 bytes a row) in a private WM x 128-byte region
+    // of the staging area, the 16-byte chunk index XOR-swizzled by bits 1-3 of
+    // the row, and writes them out itself: a wave's LDS accesses complete in
+    // order, so conversion and write-out need no block barrier between them,
+    // and the waves drift apart, one converting while another stores.
+    constexpr bool kWaveLocal = kSplitN && kSegCols * 2 == 128 && C::WM * 128 * C::kWaves <= C::kTileBytes;
     static_assert(kSplitN || (BM / C::WM) % PASSES == 0, "each pass holds whole wave rows");
     static_assert(kRows * kChunks % C::kThreads == 0, "whole write-out passes over the block");
     using OS = typename DType<ODT>::storage;
@@ -566,14 +574,81 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
                     uint2 pk;
                     pk.x = DType<ODT>::store2(v[0], v[1]);
                     pk.y = DType<ODT>::store2(v[2], v[3]);
-                    const int ml = wave_m + j * 32 + lane_m - (kSplitN ? 0 : p * kRows);
-                    *reinterpret_cast<uint2*>(stage + ml * kRowBytes + (chunk ^ out_swz<kPassCols>(ml)) * 16 +
-                                              half * 8) = pk;
+                    if constexpr (kWaveLocal) {
+                        const int rw = j * 32 + lane_m, cw = (i - i0) * 4 + g;
+                        *reinterpret_cast<uint2*>(stage + wave * (C::WM * 128) + rw * 128 +
+                                                  (cw ^ ((rw >> 1) & 7)) * 16 + half * 8) = pk;
+                    } else {
+                        const int ml = wave_m + j * 32 + lane_m - (kSplitN ? 0 : p * kRows);
+                        *reinterpret_cast<uint2*>(stage + ml * kRowBytes + (chunk ^ out_swz<kPassCols>(ml)) * 16 +
+                                                  half * 8) = pk;
+                    }
                 });
             });
         }
-        lds_barrier();
+        if constexpr (kWaveLocal) asm volatile("" ::: "memory");
+        else lds_barrier();
         if constexpr (p == 0) before_store();
+        // GELU, the residual and the store of the 8 outputs of chunk v at (m, n)
+        auto finish = [&](uint4 v, int m, int n) {
+            if constexpr (GeluLut<C, ODT, MODE, GELU>::kUse) {
+                using Lut = GeluLut<C, ODT, MODE, GELU>;
+                v = gelu_bf16x8_lut(v, lds_address(lds - Lut::kRing));
+            } else if constexpr (GELU) {
+                // every thread of the block takes part here (in the
+                // conversion above only the waves of the pass do)
+                v.x = gelu_x2<ODT>(v.x);
+                v.y = gelu_x2<ODT>(v.y);
+                v.z = gelu_x2<ODT>(v.z);
+                v.w = gelu_x2<ODT>(v.w);
+            }
+            if constexpr (MODE == 2) {
+                const uint4 rv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.resid) +
+                                                                 static_cast<int64_t>(m) * N + n);
+                uint4 sv4;
+                if (res.rs_size == 1) {
+                    const uint32_t s1 = static_cast<const OS*>(res.rscale)[0];
+                    sv4.x = sv4.y = sv4.z = sv4.w = s1 | (s1 << 16);
+                } else {
+                    sv4 = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.rscale) + n);
+                }
+                auto lo = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w & 0xffffu)); };
+                auto hi = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w >> 16)); };
+                auto fuse = [&](uint32_t lin, uint32_t s, uint32_t rr) {
+                    return DType<ODT>::store2(fmaf(lo(lin), lo(s), lo(rr)), fmaf(hi(lin), hi(s), hi(rr)));
+                };
+                v.x = fuse(v.x, sv4.x, rv.x);
+                v.y = fuse(v.y, sv4.y, rv.y);
+                v.z = fuse(v.z, sv4.z, rv.z);
+                v.w = fuse(v.w, sv4.w, rv.w);
+            }
+            *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
+        };
+        if constexpr (kWaveLocal) {
+            // lane: chunk c of rows r0, r0 + 8, ... of the wave's region
+            const int8_t* const mine = stage + wave * (C::WM * 128);
+            const int c = ln % 8, r0 = ln / 8;
+            const int n = n_base + wave_n + p * 64 + c * 8;
+            auto staged_w = [&](int r) {
+                return *reinterpret_cast<const uint4*>(mine + r * 128 + (c ^ ((r >> 1) & 7)) * 16);
+            };
+            constexpr int kSteps = C::WM / 8;
+            uint4 v_next = staged_w(r0);
+#pragma unroll 4
+            for (int step = 0; step < kSteps; ++step) {
+                const uint4 v = v_next;
+                const int r = r0 + step * 8;
+                v_next = staged_w(step + 1 < kSteps ? r + 8 : r);
+                const int m = m_base + wave_m + r;
+                if (m < M && n < N) finish(v, m, n);
+            }
+            // the next pass's conversion overwrites the region after these
+            // reads (in order); the caller reuses the staging area after the
+            // last pass
+            if constexpr (p + 1 == PASSES) lds_barrier();
+            else asm volatile("" ::: "memory");
+            return;
+        }
         // Thread tv takes chunk c = tv % kChunks of rows r0, r0 + kRowStep, ...
         // (r0 = tv / kChunks) when the block covers whole rows per step, so
         // the column, the bounds check on it and the row addresses are set up
@@ -615,40 +690,7 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
             const int m = m_nx, n = n_nx;
             coords(step + 1 < kSteps ? step + 1 : step, r_nx, c_nx, m_nx, n_nx);
             v_next = staged(r_nx, c_nx);
-            if (m < M && n < N) {
-                if constexpr (GeluLut<C, ODT, MODE, GELU>::kUse) {
-                    using Lut = GeluLut<C, ODT, MODE, GELU>;
-                    v = gelu_bf16x8_lut(v, lds_address(lds - Lut::kRing));
-                } else if constexpr (GELU) {
-                    // every thread of the block takes part here (in the
-                    // conversion above only the waves of the pass do)
-                    v.x = gelu_x2<ODT>(v.x);
-                    v.y = gelu_x2<ODT>(v.y);
-                    v.z = gelu_x2<ODT>(v.z);
-                    v.w = gelu_x2<ODT>(v.w);
-                }
-                if constexpr (MODE == 2) {
-                    const uint4 rv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.resid) +
-                                                                     static_cast<int64_t>(m) * N + n);
-                    uint4 sv4;
-                    if (res.rs_size == 1) {
-                        const uint32_t s1 = static_cast<const OS*>(res.rscale)[0];
-                        sv4.x = sv4.y = sv4.z = sv4.w = s1 | (s1 << 16);
-                    } else {
-                        sv4 = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.rscale) + n);
-                    }
-                    auto lo = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w & 0xffffu)); };
-                    auto hi = [](uint32_t w) { return DType<ODT>::load(static_cast<OS>(w >> 16)); };
-                    auto fuse = [&](uint32_t lin, uint32_t s, uint32_t rr) {
-                        return DType<ODT>::store2(fmaf(lo(lin), lo(s), lo(rr)), fmaf(hi(lin), hi(s), hi(rr)));
-                    };
-                    v.x = fuse(v.x, sv4.x, rv.x);
-                    v.y = fuse(v.y, sv4.y, rv.y);
-                    v.z = fuse(v.z, sv4.z, rv.z);
-                    v.w = fuse(v.w, sv4.w, rv.w);
-                }
-                *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
-            }
+            if (m < M && n < N) finish(v, m, n);
         }
         lds_barrier();
     });
