@@ -19,7 +19,7 @@ void launch_gemv(const int8_t* q, const int8_t* w, const float* xs, const float*
 void launch_gemm(const int8_t* q, const int8_t* w, const float* xs, const float* ws,
                  int64_t ws_size, const void* bias, const Residual* res, void* out, int out_dtype,
                  int64_t M, int64_t N, int64_t K, bool gelu, bool int32_out, int tile, hipStream_t stream);
-int gemm_config(int64_t M, int64_t N, int64_t K, int requested);
+int gemm_config(int64_t M, int64_t N, int64_t K, int requested, bool gelu);
 void launch_residual(void* out, const void* resid, const void* rscale, int64_t rs_size, int dtype,
                      int64_t M, int64_t N, hipStream_t stream);
 bool launch_gemm_xq(const void* x, int x_dtype, const float* xs, const int8_t* w, const float* ws,
@@ -381,7 +381,7 @@ int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const f
 
 int w8a8_gemm_config(int64_t M, int64_t N, int64_t K, uint32_t flags) {
     if (M < 0 || N < 0 || K < 0 || (flags & ~kKnownFlags) || tile_of(flags) > W8A8_GEMM_TILE_GENERIC) return -1;
-    return w8a8::gemm_config(M, N, K, tile_of(flags));
+    return w8a8::gemm_config(M, N, K, tile_of(flags), (flags & W8A8_ACT_GELU_TANH) != 0);
 }
 
 int w8a8_gemm_dequant_residual(const int8_t* q, const int8_t* w, const float* xs, const float* ws,

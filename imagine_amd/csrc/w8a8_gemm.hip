@@ -28,29 +28,34 @@ int device_cus() {
 
 // Default tile choice among the three one-block-per-CU configurations: the
 // estimated time of a shape is (rounds of tiles over the CUs) x (tile area),
-// divided by the configuration's measured per-area speed (relative to
-// 256 x 192, the mean over the DiT's QKV / out / FFN-up / FFN-down GEMMs at
-// M = 11712 and 19904: 256 x 256 1.10, 384 x 192 1.09; both load 15% fewer
-// bytes per MFMA operation than 256 x 192; with these factors the choice is
-// the fastest measured, or within 1% of it, at all eight).  192-token tiles cut
-// M = 11712 exactly; 384 x 192 tiles fill the N = 3072 GEMMs in 2 rounds of
-// 488 tiles (95%), where 256 x 256 makes 552 tiles (3 rounds, 72% full).
-static int default_tile(int64_t M, int64_t N) {
+// divided by the configuration's measured per-area speed relative to
+// 256 x 192.  Without GELU (the mean over the DiT's QKV / out / FFN-down
+// GEMMs at M = 11712 and 19904): 256 x 256 1.10, 384 x 192 1.09; both load
+// 15% fewer bytes per MFMA operation than 256 x 192.  With the GELU epilogue
+// (FFN-up at both M, same box): 256 x 256 1.07, 384 x 192 0.975, whose LDS
+// has no room for the GELU table and whose write-out evaluates the formula.
+// With these factors the choice is the fastest measured, or within 1% of it,
+// at all eight shapes.  192-token tiles cut M = 11712 exactly; 384 x 192
+// tiles fill the N = 3072 GEMMs in 2 rounds of 488 tiles (95%), where
+// 256 x 256 makes 552 tiles (3 rounds, 72% full).
+static int default_tile(int64_t M, int64_t N, bool gelu) {
     const int64_t cus = device_cus();
     auto cost = [&](int64_t bn, int64_t bm, double speed) {
         const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
         return static_cast<double>((tiles + cus - 1) / cus) * static_cast<double>(bn * bm) / speed;
     };
-    const double c0 = cost(256, 192, 1.0), c1 = cost(256, 256, 1.10), c2 = cost(384, 192, 1.09);
+    const double c0 = cost(256, 192, 1.0), c1 = cost(256, 256, gelu ? 1.07 : 1.10),
+                 c2 = cost(384, 192, gelu ? 0.975 : 1.09);
     if (c1 < c0 && c1 <= c2) return W8A8_GEMM_TILE_256x256;
     if (c2 < c0) return W8A8_GEMM_TILE_384x192;
     return W8A8_GEMM_TILE_256x192;
 }
 
-// The main loop w8a8_gemm_dequant runs for a shape (operands 16-byte aligned)
-// and a requested tile (W8A8_GEMM_TILE_* code, AUTO = by shape).  A requested
-// DMA tile that does not take the shape falls back to the automatic choice.
-int gemm_config(int64_t M, int64_t N, int64_t K, int requested) {
+// The main loop w8a8_gemm_dequant runs for a shape (operands 16-byte aligned),
+// its epilogue (GELU or not) and a requested tile (W8A8_GEMM_TILE_* code,
+// AUTO = by shape).  A requested DMA tile that does not take the shape falls
+// back to the automatic choice.
+int gemm_config(int64_t M, int64_t N, int64_t K, int requested, bool gelu) {
     if (!(K % 16 == 0 && M < (1ll << 31) / 2 && N < (1ll << 31) / 2 && M * K < (1ll << 40)))
         return W8A8_GEMM_TILE_GENERIC;
     switch (requested) {
@@ -62,7 +67,7 @@ int gemm_config(int64_t M, int64_t N, int64_t K, int requested) {
         case W8A8_GEMM_TILE_GENERIC: return requested;
         default: break;
     }
-    const int tile = default_tile(M, N);
+    const int tile = default_tile(M, N, gelu);
     if (tile == W8A8_GEMM_TILE_256x256 && dma_fits<CfgN256M256W8>(K)) return tile;
     if (tile == W8A8_GEMM_TILE_384x192 && dma_fits<CfgN384M192W8>(K)) return tile;
     if (dma_fits<CfgN256M192W8>(K)) return W8A8_GEMM_TILE_256x192;

@@ -64,9 +64,9 @@ inline bool dma_fits(int64_t K) {
     return K % C::BK == 0 && rows * K < (1ll << 31) - 4096;
 }
 
-// The main loop chosen for a shape and a requested W8A8_GEMM_TILE_* code
-// (w8a8_gemm.hip).
-int gemm_config(int64_t M, int64_t N, int64_t K, int requested);
+// The main loop chosen for a shape, its epilogue and a requested
+// W8A8_GEMM_TILE_* code (w8a8_gemm.hip).
+int gemm_config(int64_t M, int64_t N, int64_t K, int requested, bool gelu);
 
 // One output mode of one output dtype: the configuration gemm_config picks
 // (the generic kernel also for unaligned operands).
@@ -75,7 +75,7 @@ void gemm_dispatch(const int8_t* q, const int8_t* w, const float* xs, const floa
                           int64_t ws_size, const void* bias, const Residual& res, void* out, int64_t M,
                           int64_t N, int64_t K, int requested, hipStream_t stream) {
     const bool aligned = reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0;
-    const int cfg = aligned ? gemm_config(M, N, K, requested) : W8A8_GEMM_TILE_GENERIC;
+    const int cfg = aligned ? gemm_config(M, N, K, requested, GELU) : W8A8_GEMM_TILE_GENERIC;
     switch (cfg) {
         case W8A8_GEMM_TILE_256x192:
             launch_dma<CfgN256M192W8, ODT, MODE, GELU>(q, w, xs, ws, ws_size, bias, res, out, M, N, K, stream);

@@ -127,7 +127,8 @@ int w8a8_gemm_dequant(const int8_t* q, const int8_t* w, const float* xs, const f
                       int64_t M, int64_t N, int64_t K, uint32_t flags, hipStream_t stream);
 
 /* The W8A8_GEMM_TILE_* code of the main loop w8a8_gemm_dequant launches for
- * M x N x K with these flags (its tile bits), for 16-byte aligned operands
+ * M x N x K with these flags (its tile bits and W8A8_ACT_GELU_TANH, which
+ * changes the automatic choice), for 16-byte aligned operands
  * (unaligned ones take W8A8_GEMM_TILE_GENERIC), on the current device.  A
  * query with no reference counterpart: tests use it to know which kernel ran. */
 int w8a8_gemm_config(int64_t M, int64_t N, int64_t K, uint32_t flags);

@@ -154,7 +154,7 @@ FULL = [
     ("out_M11712", 11712, 3072, 3072, False, "384x192"),
     ("ffn_down_M11712", 11712, 12288, 3072, False, "384x192"),
     ("qkv_M19904", 19904, 3072, 9216, False, "256x256"),
-    ("ffn_up_M19904", 19904, 3072, 12288, True, "384x192"),
+    ("ffn_up_M19904", 19904, 3072, 12288, True, "256x256"),
     ("out_M19904", 19904, 3072, 3072, False, "256x256"),
     ("ffn_down_M19904", 19904, 12288, 3072, False, "256x256"),
 ]
@@ -187,7 +187,7 @@ def test_full_size_gemm_sampled_rows_bit_exact(name, m, k, n, gelu, tile):
 def test_dit_block_ffn_chain_M19904_sampled_rows_bit_exact():
     """The FFN half of a DiT block at M = 19904 (2 x (5600 + 4096 + 256)
     tokens): fused modulated norm + quantizer -> FFN-up GEMM with the GELU
-    epilogue (384 x 192 tiles) -> quantizer -> FFN-down GEMM (256 x 256 tiles)
+    epilogue (256 x 256 tiles) -> quantizer -> FFN-down GEMM (256 x 256 tiles)
     -> gated residual.  The oracle follows the same chain on 24 sampled rows
     from the library's codes of each stage: GEMM + epilogue + GELU,
     requantization of the whole 12288-wide row, second GEMM, gated residual,
@@ -202,7 +202,7 @@ def test_dit_block_ffn_chain_M19904_sampled_rows_bit_exact():
     b_down = (torch.randn(D, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
     zero = torch.zeros(B, 1, D, device=DEV, dtype=torch.bfloat16)
     q2, s2 = W.modulated_norm_quant(x, (mod[0], mod[1]), prefix, zero, 1e-6)
-    assert W.gemm_config(B * T, F, D, gelu=True) == "384x192"
+    assert W.gemm_config(B * T, F, D, gelu=True) == "256x256"
     assert W.gemm_config(B * T, D, F) == "256x256"
     up = W.gemm_dequant(q2, w_up, s2, ws_up, b_up, torch.bfloat16, gelu=True)
     q3, s3 = W.quantize_rowwise(up)

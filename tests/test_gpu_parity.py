@@ -265,8 +265,8 @@ def test_gemm_full_size_sampled_rows_bit_exact():
 @pytest.mark.parametrize("mode", ["bf16", "bf16_gelu", "f16", "f32", "bf16_residual", "int32"])
 def test_gemm_n3072_tiles_sampled_rows(mode):
     """M = 11712, N = 3072 (the out-proj / FFN-down width, where the default
-    tile choice takes 384 x 192 tiles), K = 512: every epilogue mode on 64
-    sampled rows against the oracle, bit for bit."""
+    tile choice takes 384 x 192 tiles, 256 x 192 with GELU), K = 512: every
+    epilogue mode on 64 sampled rows against the oracle, bit for bit."""
     m, k, n = 11712, 512, 3072
     odt = {"bf16_gelu": "bf16", "bf16_residual": "bf16", "int32": "f32"}.get(mode, mode)
     x = make_x(m, k, "bf16", seed=61)
