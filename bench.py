@@ -232,7 +232,7 @@ def main():
     # quantizers read their rows from HBM, not from the 256 MB Infinity Cache.
     xsets = [[torch.randn(M_TOK, HID, device=dev, generator=torch.Generator(device=dev).manual_seed(3 * i + j + 1))
               .to(torch.bfloat16) for j in range(3)] for i in range(N_SETS)]
-    x_qkv, _, x_ffn = xsets[0]
+    x_ffn = xsets[0][2]
     qbuf = {k: torch.empty((M_TOK, k), dtype=torch.int8, device=dev) for k in (HID, FFN)}
     sbuf = torch.empty((M_TOK, 1), dtype=torch.float32, device=dev)
     outs = {name: torch.empty((M_TOK, n), dtype=torch.bfloat16, device=dev) for name, _, n, *_ in layers}
@@ -292,7 +292,7 @@ def main():
     check = validate_step(layers, xsets[(nstep[0] - 1) % N_SETS][2], qbuf, sbuf, outs)
     print(f"[bench] outputs of the last timed step: {check}", file=sys.stderr, flush=True)
 
-    extras = measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv)
+    extras = measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, xsets[0])
     if not args.no_dit_step:
         extras["dit_step_60_blocks_M19904"] = measure_dit_step(W, dev)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
@@ -360,12 +360,18 @@ def traffic_bytes():
     return None
 
 
-def measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_qkv):
+def measure_extras(W, lib, dev, layers, quant, gemm, qbuf, sbuf, outs, x_in):
     ex = {}
     stream = lambda: torch.cuda.current_stream().cuda_stream
-    # per-linear GEMM (no quant), reference timing method
-    for layer in layers:
+    # per-linear GEMM (no quant), reference timing method, each on the codes
+    # and scales of its own input: FFN-down first, on the last step's
+    # quantized FFN-up output, then QKV, out-proj and FFN-up, each after
+    # quantizing its input
+    own_input = {"qkv": x_in[0], "out": x_in[1], "up": x_in[2]}
+    for layer in [layers[3]] + layers[:3]:
         name, k, n, gelu, *_ = layer
+        if name in own_input:
+            quant(own_input[name], qbuf[k])
         q = qbuf[k]
         ms = median_of_batches(lambda i: gemm(q, layer, outs[name], gelu), warmup=5, batches=5, calls=10)
         tops = 2 * M_TOK * k * n / (ms * 1e-3) / 1e12

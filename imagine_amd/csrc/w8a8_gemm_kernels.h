@@ -634,7 +634,7 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
             };
             constexpr int kSteps = C::WM / 8;
             uint4 v_next = staged_w(r0);
-#pragma unroll 4
+#pragma unroll
             for (int step = 0; step < kSteps; ++step) {
                 const uint4 v = v_next;
                 const int r = r0 + step * 8;
