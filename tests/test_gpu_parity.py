@@ -436,11 +436,15 @@ def _residual_inputs(m, n, odt, seed):
 @pytest.mark.parametrize("shape", [(300, 512, 768), (11712, 3072, 3072)])
 def test_gemm_residual_epilogue_bit_exact(odt, rs_scalar, shape):
     """GEMM + dequant + residual, bit for bit against the oracle's
-    O(fma(O(lin), rscale, resid)) on the whole output (full size: the out-proj
-    shape of the DiT block)."""
+    O(fma(O(lin), rscale, resid)) on the whole output (full size, the out-proj
+    shape of the DiT block: the whole bf16 output, 64 sampled rows of the
+    fp16 and fp32 ones)."""
     m, n, k = shape
     if m > 1000 and odt != "bf16":
-        pytest.skip("full size checked for bf16 only")
+        rows = np.sort(np.random.default_rng(7).choice(m, 64, replace=False))
+        rows[0], rows[-1] = 0, m - 1
+    else:
+        rows = np.arange(m)
     x = make_x(m, k, "bf16", seed=31)
     q_ref, xs_ref = O.quant_rowwise(storage(x, "bf16"), "bf16")
     w = make_w(n, k, seed=32)
@@ -451,9 +455,9 @@ def test_gemm_residual_epilogue_bit_exact(odt, rs_scalar, shape):
         rscale = rscale[:1]
     out = W.gemm_dequant_residual(torch.from_numpy(q_ref).to(DEV), w.to(DEV), torch.from_numpy(xs_ref).to(DEV),
                                   ws.to(DEV), bias.to(DEV), TD[odt], resid.to(DEV), rscale.to(DEV))
-    lin = O.epilogue_kitchen(O.gemm_i32(q_ref, w.numpy()), xs_ref, ws.numpy(), storage(bias, odt), odt)
-    want = O.residual(lin, storage(resid, odt), storage(rscale, odt), odt)
-    assert np.array_equal(storage(out, odt), want)
+    lin = O.epilogue_kitchen(O.gemm_i32(q_ref[rows], w.numpy()), xs_ref[rows], ws.numpy(), storage(bias, odt), odt)
+    want = O.residual(lin, storage(resid, odt)[rows], storage(rscale, odt), odt)
+    assert np.array_equal(storage(out, odt)[rows], want)
 
 
 def test_gemm_residual_unaligned_operands_take_the_direct_epilogue():
