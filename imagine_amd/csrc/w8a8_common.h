@@ -242,8 +242,8 @@ __device__ __forceinline__ uint4 gelu_bf16x8_lut(uint4 v, uint32_t base) {
         const u16x2 d = __builtin_bit_cast(u16x2, w[k]) - lo2;
         const uint32_t q = __builtin_bit_cast(uint32_t, static_cast<u16x2>((d << 2) | (d >> 14)));
         miss |= __builtin_bit_cast(uint32_t, d);
-        off[2 * k] = (q & 0xffffu) | base;
-        off[2 * k + 1] = (q >> 16) | base;
+        off[2 * k] = (q & 0xffffu) + base;
+        off[2 * k + 1] = (q >> 16) + base;
     }
     u16x2 g[4];
 #pragma unroll
