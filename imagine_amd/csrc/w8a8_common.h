@@ -229,8 +229,8 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 // GELU of 8 bf16 values (a 16-byte chunk): table lookups when all 8 are in the
 // table's range, else gelu_bf16x2 for the whole chunk.  `base` is the table's
 // LDS address; [base, base + 64 KB) lies inside the block's LDS.  All eight
-// lookups are issued before the first result is used, each pair into the two
-// halves of one register.
+// lookups are issued before the first result is used; each pair's results
+// are packed into one word.
 __device__ __forceinline__ uint4 gelu_bf16x8_lut(uint4 v, uint32_t base) {
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     typedef const __attribute__((address_space(3))) unsigned short* lds_u16;
