@@ -202,7 +202,7 @@ __device__ __forceinline__ uint32_t gelu_x2(uint32_t p) {
 // bf16 GELU by lookup in a 16 KB LDS table of gelu_bf16x2's own results, for
 // the VALU-bound epilogue of the GEMM.  Word u of the table holds the GELU of
 // the patterns kGeluLutLo + u (low half) and 0x8000 | (kGeluLutLo + u) (high
-// half): magnitudes 2^-22 up to 2^10 of either sign.  For a pattern b,
+// half): magnitudes 2^-18 up to 2^14 of either sign.  For a pattern b,
 // d = (b - kGeluLutLo) mod 2^16 is in range iff bits 12-14 of d are clear,
 // and its entry's byte offset is then (4 d mod 2^16) | (d >> 14) = 4u + 2s, s
 // the sign: both halves of a word are offset by the same three packed 16-bit
@@ -210,7 +210,7 @@ __device__ __forceinline__ uint32_t gelu_x2(uint32_t p) {
 // inside a block LDS array of at least 64 KB with the table at its start.
 // Filled per block from gelu_bf16x2, the lookup equals gelu_bf16x2 bit for
 // bit wherever it applies.
-constexpr uint32_t kGeluLutLo = 0x3480u;        // bf16 2^-22
+constexpr uint32_t kGeluLutLo = 0x3680u;        // bf16 2^-18
 constexpr int kGeluLutBytes = 4096 * 4;
 
 // Fills the table: thread t of nthreads writes words t, t + nthreads, ...

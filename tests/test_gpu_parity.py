@@ -378,7 +378,7 @@ def test_gemm_gelu_epilogue_every_preactivation(odt, tile):
     tail, subnormals and signed zeros included).  Bit for bit against the
     oracle, on the staged epilogue of each DMA tile with one block per CU
     (256x256 and 256x192 look bf16 GELU up in an LDS table for magnitudes
-    2^-22 to 2^10, 384x192 evaluates it), of the two-blocks-per-CU one
+    2^-18 to 2^14, 384x192 evaluates it), of the two-blocks-per-CU one
     (256x128), and on the register-staged and generic main loops."""
     bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
     bits = bits[np.isfinite(O.to_f32(bits, odt))]
