@@ -226,6 +226,55 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
     return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
 }
 
+// Table offsets of the 8 bf16 values of a chunk (see gelu_bf16x8_lut); `miss`
+// collects the bits that flag an out-of-range value (0x70007000).
+__device__ __forceinline__ void gelu_lut_offsets(uint4 v, uint32_t base, uint32_t (&off)[8], uint32_t& miss) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    const u16x2 lo2 = {static_cast<unsigned short>(kGeluLutLo), static_cast<unsigned short>(kGeluLutLo)};
+    miss = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const u16x2 d = __builtin_bit_cast(u16x2, w[k]) - lo2;
+        const uint32_t q = __builtin_bit_cast(uint32_t, static_cast<u16x2>((d << 2) | (d >> 14)));
+        miss |= __builtin_bit_cast(uint32_t, d);
+        off[2 * k] = (q & 0xffffu) + base;
+        off[2 * k + 1] = (q >> 16) + base;
+    }
+}
+
+// GELU of two chunks, all 16 lookups issued before the first result is used
+// (otherwise as gelu_bf16x8_lut).
+__device__ __forceinline__ void gelu_bf16x16_lut(uint4& a, uint4& b, uint32_t base) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    typedef const __attribute__((address_space(3))) unsigned short* lds_u16;
+    uint32_t oa[8], ob[8], ma, mb;
+    gelu_lut_offsets(a, base, oa, ma);
+    gelu_lut_offsets(b, base, ob, mb);
+    u16x2 ga[4], gb[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        ga[k].x = *(lds_u16)static_cast<uintptr_t>(oa[2 * k]);
+        ga[k].y = *(lds_u16)static_cast<uintptr_t>(oa[2 * k + 1]);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        gb[k].x = *(lds_u16)static_cast<uintptr_t>(ob[2 * k]);
+        gb[k].y = *(lds_u16)static_cast<uintptr_t>(ob[2 * k + 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 ra = make_uint4(__builtin_bit_cast(uint32_t, ga[0]), __builtin_bit_cast(uint32_t, ga[1]),
+                          __builtin_bit_cast(uint32_t, ga[2]), __builtin_bit_cast(uint32_t, ga[3]));
+    uint4 rb = make_uint4(__builtin_bit_cast(uint32_t, gb[0]), __builtin_bit_cast(uint32_t, gb[1]),
+                          __builtin_bit_cast(uint32_t, gb[2]), __builtin_bit_cast(uint32_t, gb[3]));
+    if (__builtin_expect((ma & 0x70007000u) != 0, 0))
+        ra = make_uint4(gelu_bf16x2(a.x), gelu_bf16x2(a.y), gelu_bf16x2(a.z), gelu_bf16x2(a.w));
+    if (__builtin_expect((mb & 0x70007000u) != 0, 0))
+        rb = make_uint4(gelu_bf16x2(b.x), gelu_bf16x2(b.y), gelu_bf16x2(b.z), gelu_bf16x2(b.w));
+    a = ra;
+    b = rb;
+}
+
 // GELU of 8 bf16 values (a 16-byte chunk): table lookups when all 8 are in the
 // table's range, else gelu_bf16x2 for the whole chunk.  `base` is the table's
 // LDS address; [base, base + 64 KB) lies inside the block's LDS.  All eight

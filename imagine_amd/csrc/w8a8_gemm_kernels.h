@@ -589,19 +589,8 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
         if constexpr (kWaveLocal) asm volatile("" ::: "memory");
         else lds_barrier();
         if constexpr (p == 0) before_store();
-        // GELU, the residual and the store of the 8 outputs of chunk v at (m, n)
-        auto finish = [&](uint4 v, int m, int n) {
-            if constexpr (GeluLut<C, ODT, MODE, GELU>::kUse) {
-                using Lut = GeluLut<C, ODT, MODE, GELU>;
-                v = gelu_bf16x8_lut(v, lds_address(lds - Lut::kRing));
-            } else if constexpr (GELU) {
-                // every thread of the block takes part here (in the
-                // conversion above only the waves of the pass do)
-                v.x = gelu_x2<ODT>(v.x);
-                v.y = gelu_x2<ODT>(v.y);
-                v.z = gelu_x2<ODT>(v.z);
-                v.w = gelu_x2<ODT>(v.w);
-            }
+        // the residual and the store of the 8 outputs of chunk v at (m, n)
+        auto finish_plain = [&](uint4 v, int m, int n) {
             if constexpr (MODE == 2) {
                 const uint4 rv = *reinterpret_cast<const uint4*>(static_cast<const OS*>(res.resid) +
                                                                  static_cast<int64_t>(m) * N + n);
@@ -624,6 +613,21 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
             }
             *reinterpret_cast<uint4*>(static_cast<OS*>(out) + static_cast<int64_t>(m) * N + n) = v;
         };
+        // GELU, the residual and the store of the 8 outputs of chunk v at (m, n)
+        auto finish = [&](uint4 v, int m, int n) {
+            if constexpr (GeluLut<C, ODT, MODE, GELU>::kUse) {
+                using Lut = GeluLut<C, ODT, MODE, GELU>;
+                v = gelu_bf16x8_lut(v, lds_address(lds - Lut::kRing));
+            } else if constexpr (GELU) {
+                // every thread of the block takes part here (in the
+                // conversion above only the waves of the pass do)
+                v.x = gelu_x2<ODT>(v.x);
+                v.y = gelu_x2<ODT>(v.y);
+                v.z = gelu_x2<ODT>(v.z);
+                v.w = gelu_x2<ODT>(v.w);
+            }
+            finish_plain(v, m, n);
+        };
         if constexpr (kWaveLocal) {
             // lane: chunk c of rows r0, r0 + 8, ... of the wave's region
             const int8_t* const mine = stage + wave * (C::WM * 128);
@@ -633,14 +637,34 @@ __device__ __forceinline__ void store_tiles_staged(const v16i (&acc)[C::TN][C::T
                 return *reinterpret_cast<const uint4*>(mine + r * 128 + (c ^ ((r >> 1) & 7)) * 16);
             };
             constexpr int kSteps = C::WM / 8;
-            uint4 v_next = staged_w(r0);
+            if constexpr (GeluLut<C, ODT, MODE, GELU>::kUse && kSteps % 2 == 0) {
+                // two chunks per step: their 16 lookups in flight together;
+                // GELU of rows past M is computed and not stored
+                using Lut = GeluLut<C, ODT, MODE, GELU>;
+                uint4 n0 = staged_w(r0), n1 = staged_w(r0 + 8);
 #pragma unroll
-            for (int step = 0; step < kSteps; ++step) {
-                const uint4 v = v_next;
-                const int r = r0 + step * 8;
-                v_next = staged_w(step + 1 < kSteps ? r + 8 : r);
-                const int m = m_base + wave_m + r;
-                if (m < M && n < N) finish(v, m, n);
+                for (int step = 0; step < kSteps; step += 2) {
+                    uint4 v0 = n0, v1 = n1;
+                    const int r = r0 + step * 8;
+                    if (step + 2 < kSteps) {
+                        n0 = staged_w(r + 16);
+                        n1 = staged_w(r + 24);
+                    }
+                    gelu_bf16x16_lut(v0, v1, lds_address(lds - Lut::kRing));
+                    const int m = m_base + wave_m + r;
+                    if (m < M && n < N) finish_plain(v0, m, n);
+                    if (m + 8 < M && n < N) finish_plain(v1, m + 8, n);
+                }
+            } else {
+                uint4 v_next = staged_w(r0);
+#pragma unroll
+                for (int step = 0; step < kSteps; ++step) {
+                    const uint4 v = v_next;
+                    const int r = r0 + step * 8;
+                    v_next = staged_w(step + 1 < kSteps ? r + 8 : r);
+                    const int m = m_base + wave_m + r;
+                    if (m < M && n < N) finish(v, m, n);
+                }
             }
             // the next pass's conversion overwrites the region after these
             // reads (in order); the caller reuses the staging area after the
